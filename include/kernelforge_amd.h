@@ -1,0 +1,178 @@
+/*
+ * kernelforge_amd C ABI.
+ *
+ * Plain C entry points for the three operator hot paths of KernelForge
+ * (RMSNorm, SANA ReLU linear attention, FlashAttention forward/JVP),
+ * implemented as hand-written HIP kernels for gfx950 (MI355X).
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers owned by the caller.  The library never
+ *     allocates device memory; SANA's cross-split partials live in a caller
+ *     supplied workspace whose size is given by kf_linattn_workspace_bytes.
+ *   - Tensors are dense and row-major (the innermost dimension is contiguous)
+ *     in the layouts documented per function.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Launches are
+ *     asynchronous, never synchronise the device and never call hipMalloc,
+ *     so every entry point may be captured into a HIP graph.
+ *   - The return value is KF_OK (0) on success or a kf_status code;
+ *     kf_last_error() then returns a message for the calling thread.
+ */
+#ifndef KERNELFORGE_AMD_H
+#define KERNELFORGE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_ABI_VERSION 1
+
+typedef void* kf_stream_t; /* hipStream_t */
+
+typedef enum kf_dtype {
+    KF_F32 = 0,
+    KF_F16 = 1,
+    KF_BF16 = 2
+} kf_dtype;
+
+typedef enum kf_status {
+    KF_OK = 0,
+    KF_E_INVALID = 1,     /* bad shape, dtype, pointer or argument value */
+    KF_E_UNSUPPORTED = 2, /* a valid request this build has no kernel for */
+    KF_E_WORKSPACE = 3,   /* workspace missing or too small */
+    KF_E_HIP = 4          /* a HIP runtime call or kernel launch failed */
+} kf_status;
+
+/* ABI version of the loaded library (KF_ABI_VERSION at build time). */
+int kf_abi_version(void);
+
+/* Static name of a kf_status value. */
+const char* kf_status_string(int status);
+
+/* Message describing the most recent failure on the calling thread. */
+const char* kf_last_error(void);
+
+/* ------------------------------------------------------------------ */
+/* RMSNorm                                                             */
+/* ------------------------------------------------------------------ */
+
+/*
+ * y[r, :] = dt( float(dt(x[r, :] * inv)) * float(weight[:]) ),
+ * inv = 1 / sqrt(sum_c x[r, c]^2 / dim + eps), accumulated in fp32,
+ * where dt() rounds to the storage dtype (round-to-nearest-even).
+ *
+ * Replaces the compiled callable returned by
+ *   rms_norm(batch, seq_len, dim, eps, dtype)   rmsnorm/custom.py:15-73
+ * whose rounding points follow RMSNorm.forward   rmsnorm/original.py:38,51-52.
+ *
+ * x, y: [rows, dim]; weight: [dim]; all of `dtype`.  rows >= 0, dim >= 1.
+ */
+int kf_rmsnorm_fwd(const void* x, const void* weight, void* y,
+                   int64_t rows, int64_t dim, float eps, int dtype,
+                   kf_stream_t stream);
+
+/*
+ * Weight-free fp32 RMSNorm with the two-scan baseline's semantics:
+ * b[r, :] = a[r, :] / sqrt(sum_c a[r, c]^2 / n + eps).
+ *
+ * Replaces rms_norm(A, blk_m) (the TileLang "original" baseline,
+ * rmsnorm/original.py:55-78, which hard-codes eps = 1e-12).
+ * a, b: fp32 [rows, n].
+ */
+int kf_rmsnorm_noweight_f32(const float* a, float* b, int64_t rows, int64_t n,
+                            float eps, kf_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* SANA ReLU linear attention                                          */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Sequence split count the host dispatcher uses for a shape (>= 1).
+ * Mirrors the role of the split heuristic in qkv_attn_matmul
+ * (SANA_LinearAttention/custom.py:355-368), re-derived for 256 CUs.
+ */
+int64_t kf_linattn_default_splits(int64_t batch, int64_t heads, int64_t dim,
+                                  int64_t seq_len);
+
+/* Workspace bytes kf_linattn_fwd needs for `splits` sequence splits. */
+int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int64_t dim,
+                                   int64_t splits);
+
+/*
+ * out[b, n, h*D + r] = sum_c S[r][c] relu(q)[n,c] / (sum_c z[c] relu(q)[n,c] + eps)
+ * with S = sum_n v[n,:]^T relu(k)[n,:] and z = sum_n relu(k)[n,:] per (b, h),
+ * accumulated in fp32 over `splits` sequence splits and reduced across
+ * splits in a fixed order (deterministic, no atomics on data).
+ *
+ * Replaces run(qkv) returned by
+ *   qkv_attn_matmul(batch, heads, dim, seq_len, eps, dtype, output_dtype,
+ *                   reduce_splits)          SANA_LinearAttention/custom.py:340-388
+ * with the arithmetic of LiteLA.attn_matmul SANA_LinearAttention/original.py:99-117
+ * (fp32_attention semantics) on the packed layout of
+ * LiteLA.forward                          SANA_LinearAttention/original.py:124-134.
+ *
+ * qkv: [batch, seq_len, 3, heads*dim] of in_dtype (KF_BF16 or KF_F16, or KF_F32);
+ * out: [batch, seq_len, heads*dim] of out_dtype (KF_F32, KF_F16 or KF_BF16).
+ * dim must be 32 for the MFMA kernels in this build.
+ * splits <= 0 selects kf_linattn_default_splits.
+ */
+int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
+                   int64_t workspace_bytes, int64_t batch, int64_t seq_len,
+                   int64_t heads, int64_t dim, int64_t splits, float eps,
+                   int in_dtype, int out_dtype, kf_stream_t stream);
+
+/* ------------------------------------------------------------------ */
+/* FlashAttention forward and JVP                                      */
+/* ------------------------------------------------------------------ */
+
+/*
+ * Layouts: q, tq, o, to: [B, Nq, Hq, D]; k, v, tk, tv: [B, Nk, Hkv, D];
+ * lse: fp32 [B, Hq, Nq], natural log.  dtype is KF_F16 or KF_BF16.
+ * Hq % Hkv == 0 (GQA/MQA), D % 8 == 0 and D <= 256.  causal selects the
+ * bottom-right aligned mask col <= row + Nk - Nq.  Rows with no valid key
+ * produce o = 0, to = 0 and lse = +inf.
+ */
+
+/*
+ * O and LSE.  Replaces the forward FlashAttentionFunction.forward calls
+ * (flash_attention_jvp/custom.py:229-238, flash-attn _flash_attn_forward).
+ */
+int kf_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+              int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv,
+              int64_t D, float scale, int causal, int dtype, kf_stream_t stream);
+
+/*
+ * tO from cached O and LSE:
+ *   P = exp(scale*q k^T - lse),  tS = scale*(tq k^T + q tk^T),
+ *   tO = P tv + (P*tS) v - rowsum(P*tS) * O.
+ * Any of tq, tk, tv may be NULL, meaning a zero tangent.
+ * Replaces kernelforge::flash_attention_jvp / _attention_jvp_kernel
+ * (flash_attention_jvp/custom.py:12-120, 137-152).
+ */
+int kf_fa_jvp(const void* q, const void* k, const void* v,
+              const void* tq, const void* tk, const void* tv,
+              const void* o, const float* lse, void* to,
+              int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv,
+              int64_t D, float scale, int causal, int dtype, kf_stream_t stream);
+
+/*
+ * Fused single pass: O, LSE and tO in one scan over the K/V tiles with the
+ * online recurrences of flash-attention-jvp-derivation.md:388-558
+ * (states m, l, U, r, G).  The reference implements this path as two
+ * launches (flash-attn forward + _attention_jvp_kernel,
+ * flash_attention_jvp/custom.py:229-276); this entry point replaces both.
+ * Any of tq, tk, tv may be NULL (zero tangent).
+ */
+int kf_fa_fwd_jvp(const void* q, const void* k, const void* v,
+                  const void* tq, const void* tk, const void* tv,
+                  void* o, float* lse, void* to,
+                  int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv,
+                  int64_t D, float scale, int causal, int dtype,
+                  kf_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KERNELFORGE_AMD_H */

@@ -1,0 +1,117 @@
+"""RMSNorm on gfx950: a one-pass row kernel behind the reference factory API.
+
+``rms_norm(batch, seq_len, dim, eps, dtype)`` returns a callable
+``kernel(X[batch, seq_len, dim], Weight[dim]) -> Output`` exactly like the
+TileLang factory it replaces (rmsnorm/custom.py:11-31: the output is
+allocated by the callable, ``out_idx=[-1]``).  The arithmetic is that of
+``RMSNorm.forward`` (rmsnorm/original.py:38, 51-52): fp32 sum of squares,
+``inv = 1/sqrt(mean + eps)``, then ``dt(float(dt(x*inv)) * float(w))``.
+
+The kernel (kernelforge_amd/csrc/rmsnorm.hip) reads every row once with
+16-byte vector loads into registers, reduces the sum of squares across the
+64-lane wavefront (and through LDS when a row spans several wavefronts),
+and writes the row once.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+
+from .. import _lib
+
+# dtype strings of the reference factory (torch names without "torch.").
+DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32,
+          "float": torch.float32}
+
+
+def _launch(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor, eps: float) -> None:
+    lib = _lib.load()
+    dim = x.shape[-1]
+    rows = x.numel() // dim if dim else 0
+    rc = lib.kf_rmsnorm_fwd(_lib.ptr(x), _lib.ptr(weight), _lib.ptr(out), rows, dim, float(eps),
+                            _lib.kf_dtype(x.dtype), _lib.stream_of(x))
+    _lib.check(rc, "kf_rmsnorm_fwd")
+
+
+class RMSNormKernel:
+    """Callable bound to one (batch, seq_len, dim, eps, dtype), like a compiled TileLang kernel."""
+
+    def __init__(self, batch: int, seq_len: int, dim: int, eps: float, dtype: torch.dtype):
+        self.batch, self.seq_len, self.dim = batch, seq_len, dim
+        self.eps = float(eps)
+        self.dtype = dtype
+
+    def __call__(self, X: torch.Tensor, Weight: torch.Tensor) -> torch.Tensor:
+        expect = (self.batch, self.seq_len, self.dim)
+        if tuple(X.shape) != expect or X.dtype != self.dtype:
+            raise ValueError(f"X must be {self.dtype} of shape {expect}, got {X.dtype} {tuple(X.shape)}")
+        if tuple(Weight.shape) != (self.dim,) or Weight.dtype != self.dtype:
+            raise ValueError(f"Weight must be {self.dtype} of shape ({self.dim},)")
+        if Weight.device != X.device:
+            raise ValueError("X and Weight must be on the same device")
+        _lib.require_gpu(X)
+        X = X.contiguous()
+        Weight = Weight.contiguous()
+        out = torch.empty_like(X)
+        _launch(X, Weight, out, self.eps)
+        return out
+
+
+@lru_cache(maxsize=None)
+def rms_norm(batch: int, seq_len: int, dim: int, eps: float = 1e-6, dtype: str = "bfloat16"):
+    """Return ``kernel(X, Weight) -> Output`` (rmsnorm/custom.py:15-21)."""
+    if dtype not in DTYPES:
+        raise ValueError(f"dtype must be one of {sorted(DTYPES)}, got {dtype!r}")
+    if min(batch, seq_len) < 0 or dim <= 0:
+        raise ValueError("batch and seq_len must be >= 0 and dim > 0")
+    return RMSNormKernel(batch, seq_len, dim, eps, DTYPES[dtype])
+
+
+def rms_norm_tensor(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Shape-generic functional form: normalise over the last dimension of x."""
+    if x.dim() < 1 or weight.shape != (x.shape[-1],) or weight.dtype != x.dtype:
+        raise ValueError("weight must have shape (x.shape[-1],) and x's dtype")
+    _lib.require_gpu(x, weight)
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    _launch(x, weight.contiguous(), out, eps)
+    return out
+
+
+def original_tilelang_rms_norm(A: torch.Tensor, blk_m: int = 1) -> torch.Tensor:
+    """fp32 weight-free RMSNorm with the two-scan baseline's semantics.
+
+    Mirrors ``rms_norm(A, blk_m)`` of rmsnorm/original.py:55-78: ``A`` is
+    fp32 ``[M, N]``, the result is ``A * rsqrt(sum(A^2)/N + 1e-12)``.  The
+    row-block size ``blk_m`` only affected the TileLang schedule and is
+    validated but not needed by the one-pass kernel.
+    """
+    if A.dim() != 2 or A.dtype != torch.float32:
+        raise ValueError("A must be a 2-D float32 tensor")
+    if blk_m <= 0:
+        raise ValueError("blk_m must be positive")
+    _lib.require_gpu(A)
+    A = A.contiguous()
+    B = torch.empty_like(A)
+    rc = _lib.load().kf_rmsnorm_noweight_f32(_lib.ptr(A), _lib.ptr(B), A.shape[0], A.shape[1],
+                                             1e-12, _lib.stream_of(A))
+    _lib.check(rc, "kf_rmsnorm_noweight_f32")
+    return B
+
+
+class RMSNorm(torch.nn.Module):
+    """``RMSNorm(dim, scale_factor=1.0, eps=1e-6)`` (rmsnorm/original.py:9-52) on the HIP kernel.
+
+    The weight must have the input's dtype (cast the module with ``.to``);
+    mixed-dtype promotion is not implemented and raises ValueError.
+    """
+
+    def __init__(self, dim: int, scale_factor=1.0, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = torch.nn.Parameter(torch.ones(dim) * scale_factor)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return rms_norm_tensor(x, self.weight.detach(), self.eps)
