@@ -1,0 +1,115 @@
+"""SANA ReLU linear attention parity on the GPU (HIP via the C ABI vs the CPU oracle).
+
+Mirrors SANA_LinearAttention/test.py:50-94 (packed qkv, custom vs eager) with
+the north-star tolerance (2e-2 abs / 2e-2 rel in bf16 against an fp32
+reference).  The outputs are O(1/sqrt(N)) in magnitude, so every case also
+checks the relative Frobenius error, which a dropped term or a wrong index
+would fail.
+"""
+
+import pytest
+import torch
+
+from kernelforge_amd.SANA_LinearAttention import default_splits, linear_attention, qkv_attn_matmul
+from oracle import sana as orc
+from tests._util import randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def rel_fro(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def check(out, ref, rel):
+    torch.testing.assert_close(out.float().cpu(), ref.float(), atol=2e-2, rtol=2e-2)
+    err = rel_fro(out, ref)
+    assert err < rel, f"relative Frobenius error {err:.3g} >= {rel}"
+    return err
+
+
+@pytest.mark.parametrize("B,H,N", [(2, 70, 4096), (1, 70, 16384)])
+@pytest.mark.parametrize("out_name", ["bfloat16", "float"])
+def test_baseline_configs(B, H, N, out_name):
+    """BASELINE configs 2 and 3: bf16 qkv ~ N(0,1), D = 32."""
+    qkv = randn((B, N, 3, H * 32), torch.bfloat16, seed=B * 7 + N)
+    run = qkv_attn_matmul(B, H, 32, N, 1e-15, "bfloat16", out_name)
+    out = run(qkv.to(DEV))
+    assert out.shape == (B, N, H * 32)
+    ref = orc.linear_attention(qkv, H, 32)
+    err = check(out, ref, 1e-2 if out_name == "bfloat16" else 1e-4)
+    print(f"B={B} H={H} N={N} out={out_name} rel_fro={err:.3g} max_abs={float((out.float().cpu()-ref).abs().max()):.3g}")
+
+
+@pytest.mark.parametrize("B,H,N", [(1, 1, 1), (1, 2, 63), (1, 3, 65), (2, 5, 200), (3, 4, 1000),
+                                   (1, 70, 2048), (2, 36, 1024)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_ragged_shapes(B, H, N, dtype):
+    qkv = randn((B, N, 3, H * 32), dtype, seed=N + H)
+    out = linear_attention(qkv.to(DEV), H, 32, output_dtype=torch.float32)
+    check(out, orc.linear_attention(qkv, H, 32), 1e-4)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 7, 64])
+def test_split_invariance(splits):
+    """The split count changes only the fp32 summation order."""
+    qkv = randn((1, 4096, 3, 8 * 32), torch.bfloat16, seed=11).to(DEV)
+    base = linear_attention(qkv, 8, 32, output_dtype=torch.float32, splits=1)
+    out = linear_attention(qkv, 8, 32, output_dtype=torch.float32, splits=splits)
+    assert rel_fro(out, base) < 1e-5
+    check(out, orc.linear_attention(qkv.cpu(), 8, 32), 1e-4)
+
+
+@pytest.mark.parametrize("dim", [8, 16, 64, 128])
+def test_generic_head_dims(dim):
+    H = 256 // dim
+    qkv = randn((2, 300, 3, H * dim), torch.bfloat16, seed=dim)
+    out = linear_attention(qkv.to(DEV), H, dim, output_dtype=torch.float32)
+    check(out, orc.linear_attention(qkv, H, dim), 1e-4)
+
+
+def test_fp32_input():
+    qkv = randn((1, 500, 3, 4 * 32), torch.float32, seed=3)
+    run = qkv_attn_matmul(1, 4, 32, 500, 1e-15, "float", "float")
+    check(run(qkv.to(DEV)), orc.linear_attention(qkv, 4, 32), 1e-5)
+
+
+def test_deterministic_and_linear_in_v():
+    """Two runs are bit-identical; doubling v doubles the output exactly."""
+    B, H, N = 2, 70, 4096
+    qkv = randn((B, N, 3, H * 32), torch.bfloat16, seed=21).to(DEV)
+    a = linear_attention(qkv, H, 32, output_dtype=torch.float32)
+    b = linear_attention(qkv, H, 32, output_dtype=torch.float32)
+    assert torch.equal(a, b)
+    qkv2 = qkv.clone()
+    qkv2[:, :, 2] *= 2
+    c = linear_attention(qkv2, H, 32, output_dtype=torch.float32)
+    assert torch.equal(c, 2 * a)
+
+
+def test_negative_q_gives_zero():
+    qkv = randn((1, 777, 3, 3 * 32), torch.bfloat16, seed=4)
+    qkv[:, :, 0] = -qkv[:, :, 0].abs()
+    out = linear_attention(qkv.to(DEV), 3, 32, output_dtype=torch.float32)
+    assert torch.count_nonzero(out) == 0
+
+
+def test_matches_eager_bf16_semantics():
+    """The reference test compares against eager bf16 attn_matmul at 2e-2 (test.py:79-82)."""
+    qkv = randn((1, 1024, 3, 36 * 32), torch.bfloat16, seed=5)
+    out = qkv_attn_matmul(1, 36, 32, 1024, dtype="bfloat16", output_dtype="bfloat16")(qkv.to(DEV))
+    eager = orc.linear_attention(qkv, 36, 32, fp32_attention=False)
+    torch.testing.assert_close(out.float().cpu(), eager, atol=2e-2, rtol=2e-2)
+
+
+def test_validation_and_splits():
+    with pytest.raises(ValueError, match="dim"):
+        qkv_attn_matmul(1, 2, 48, 16)
+    with pytest.raises(ValueError, match="output_dtype"):
+        qkv_attn_matmul(1, 2, 32, 16, output_dtype="int8")
+    run = qkv_attn_matmul(1, 2, 32, 16)
+    with pytest.raises(ValueError):
+        run(torch.zeros(1, 17, 3, 64, device=DEV, dtype=torch.bfloat16))
+    assert default_splits(2, 70, 32, 4096) >= 1
