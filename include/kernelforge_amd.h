@@ -143,9 +143,12 @@ int kf_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
               int64_t D, float scale, int causal, int dtype, kf_stream_t stream);
 
 /*
- * tO from cached O and LSE:
- *   P = exp(scale*q k^T - lse),  tS = scale*(tq k^T + q tk^T),
- *   tO = P tv + (P*tS) v - rowsum(P*tS) * O.
+ * tO from the cached LSE (standalone JVP, no forward launch):
+ *   P = exp(scale*q k^T - lse),  tS = scale*(tq k^T + q tk^T),  H = P*tS,
+ *   tO = P tv + H v - rowsum(H) * O.
+ * O is recomputed in fp32 from the same P inside the kernel (U = P v): the
+ * cached 16-bit `o` is accepted for interface parity and is not read,
+ * because rowsum(H) would amplify its rounding error.
  * Any of tq, tk, tv may be NULL, meaning a zero tangent.
  * Replaces kernelforge::flash_attention_jvp / _attention_jvp_kernel
  * (flash_attention_jvp/custom.py:12-120, 137-152).
