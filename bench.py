@@ -1,0 +1,320 @@
+"""Benchmark of the kernelforge_amd hot paths on one MI355X.
+
+Prints ONE JSON line.  The headline ("value") is BASELINE config 1: RMSNorm
+bf16 on x[16384, 4096] (one step = one RMSNorm pass), in HBM GB/s of
+algorithmic traffic (read x once, write y once, read w).  The same line
+carries, under "results", every BASELINE config measured the same way:
+the RMSNorm hidden sweep {2048, 4096, 8192}, SANA linear attention at both
+shapes (HBM GB/s and TFLOP/s), and FlashAttention at B=2, H=16, N=4096,
+D=128 (fused forward+JVP, standalone JVP from LSE, forward), in TFLOP/s
+against the bf16 dense MFMA peak.
+
+Timing: inputs are resident in HBM before the timed region; input/output
+sets rotate so that the bytes touched between two uses of a buffer exceed
+the 256 MB Infinity Cache; the timed region is bracketed by
+torch.cuda.synchronize() and measured with HIP events recorded on the
+stream the kernels are launched on (torch's current stream).
+
+The CPU baseline times the oracle (a plain-torch restatement of the
+reference original.py, test infrastructure) on the host cores on a bounded
+sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+BASELINE_METRIC = "RMSNorm HBM GB/s; lin-attn & FA-JVP TFLOP/s as % roofline; speedup vs ref"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 * 2**20
+
+
+def _sets_for(bytes_per_set: int) -> int:
+    """Number of rotating buffer sets so that a full rotation exceeds 2x the MALL."""
+    return max(2, min(16, -(-2 * MALL_BYTES // max(1, bytes_per_set)) + 1))
+
+
+def _time_launches(fn, n_sets: int, steps: int, warmup: int) -> float:
+    """Average microseconds per launch of fn(set_index) over `steps` launches."""
+    for i in range(warmup):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(i % n_sets)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------
+# Workloads (GPU).  Each returns a dict with the per-launch time and rates.
+# ---------------------------------------------------------------------------
+def bench_rmsnorm(hidden: int, steps: int, warmup: int, rows: int = 16384) -> dict:
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    bytes_per_launch = 2 * rows * hidden * 2 + hidden * 2
+    n_sets = _sets_for(bytes_per_launch)
+    g = _gen(hidden)
+    xs = [torch.randn(rows, hidden, generator=g).to(torch.bfloat16).to("cuda") for _ in range(n_sets)]
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to("cuda")
+    ys = [torch.empty_like(x) for x in xs]
+    stream = _lib.stream_of(xs[0])
+    args = [(_lib.ptr(xs[i]), _lib.ptr(w), _lib.ptr(ys[i])) for i in range(n_sets)]
+    fnc = lib.kf_rmsnorm_fwd
+
+    def launch(i):
+        x, wp, y = args[i]
+        rc = fnc(x, wp, y, rows, hidden, 1e-6, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_rmsnorm_fwd")
+
+    us = _time_launches(launch, n_sets, steps, warmup)
+    gbs = bytes_per_launch / (us * 1e-6) / 1e9
+    return dict(kernel="rmsnorm_vec_kernel", workload=f"rmsnorm_bf16_{rows}x{hidden}", us=us,
+                bytes=bytes_per_launch, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, sets=n_sets)
+
+
+def bench_sana(B: int, H: int, N: int, steps: int, warmup: int, D: int = 32) -> dict:
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    C = H * D
+    bytes_per_launch = 3 * B * N * C * 2 + B * N * C * 2
+    flops = 4 * B * H * N * D * (D + 1)
+    n_sets = _sets_for(bytes_per_launch)
+    g = _gen(N + B)
+    qkvs = [torch.randn(B, N, 3, C, generator=g).to(torch.bfloat16).to("cuda") for _ in range(n_sets)]
+    outs = [torch.empty(B, N, C, device="cuda", dtype=torch.bfloat16) for _ in range(n_sets)]
+    splits = int(lib.kf_linattn_default_splits(B, H, D, N))
+    ws_bytes = int(lib.kf_linattn_workspace_bytes(B, H, D, splits))
+    ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
+    stream = _lib.stream_of(ws)
+    args = [(_lib.ptr(qkvs[i]), _lib.ptr(outs[i])) for i in range(n_sets)]
+    wsp = _lib.ptr(ws)
+    fnc = lib.kf_linattn_fwd
+
+    def launch(i):
+        q, o = args[i]
+        rc = fnc(q, o, wsp, ws_bytes, B, N, H, D, splits, 1e-15, _lib.KF_BF16, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_linattn_fwd")
+
+    us = _time_launches(launch, n_sets, steps, warmup)
+    gbs = bytes_per_launch / (us * 1e-6) / 1e9
+    tflops = flops / (us * 1e-6) / 1e12
+    return dict(kernel="linattn (state+reduce+out)", workload=f"sana_bf16_B{B}_H{H}_D{D}_N{N}", us=us,
+                bytes=bytes_per_launch, flops=flops, gbs=gbs, tflops=tflops,
+                roofline_frac=gbs / HBM_PEAK_GBS, mfma_frac=tflops / BF16_PEAK_TFLOPS, splits=splits,
+                sets=n_sets)
+
+
+def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> dict:
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    g = _gen(7)
+    shape = (B, N, H, D)
+    q, k, v, tq, tk, tv = (torch.randn(shape, generator=g).to(torch.bfloat16).to("cuda") for _ in range(6))
+    o = torch.empty_like(q)
+    to = torch.empty_like(q)
+    lse = torch.empty(B, H, N, device="cuda", dtype=torch.float32)
+    scale = D ** -0.5
+    stream = _lib.stream_of(q)
+    P = [_lib.ptr(x) for x in (q, k, v, tq, tk, tv, o, lse, to)]
+    dims = (B, N, N, H, H, D, scale, 0, _lib.KF_BF16, stream)
+    if mode == "fwd_jvp":
+        fnc, a = lib.kf_fa_fwd_jvp, (*P, *dims)
+        gemms, name = 6, "fa_kernel<bf16,128,FWD_JVP>"
+    elif mode == "jvp":
+        rc = lib.kf_fa_fwd(P[0], P[1], P[2], P[6], P[7], *dims)
+        _lib.check(rc, "kf_fa_fwd")
+        fnc, a = lib.kf_fa_jvp, (*P, *dims)
+        gemms, name = 6, "fa_kernel<bf16,128,JVP>"
+    else:
+        fnc, a = lib.kf_fa_fwd, (P[0], P[1], P[2], P[6], P[7], *dims)
+        gemms, name = 2, "fa_kernel<bf16,128,FWD>"
+
+    def launch(_):
+        rc = fnc(*a)
+        if rc:
+            _lib.check(rc, name)
+
+    us = _time_launches(launch, 1, steps, warmup)
+    flops = 2 * gemms * B * H * N * N * D
+    tflops = flops / (us * 1e-6) / 1e12
+    return dict(kernel=name, workload=f"fa_{mode}_bf16_B{B}_H{H}_N{N}_D{D}", us=us, flops=flops,
+                gemm_equivalents=gemms, tflops=tflops, roofline_frac=tflops / BF16_PEAK_TFLOPS)
+
+
+def bench_copy(steps: int, warmup: int) -> dict:
+    """Device-to-device copy of 256 MiB: the achievable HBM stream ceiling."""
+    n = 128 * 2**20  # bf16 elements = 256 MiB
+    n_sets = 4
+    src = [torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_() for _ in range(n_sets)]
+    dst = [torch.empty_like(s) for s in src]
+    us = _time_launches(lambda i: dst[i].copy_(src[i]), n_sets, steps, warmup)
+    return dict(kernel="torch copy_", workload="copy_bf16_256MiB", bytes=4 * n, us=us,
+                gbs=4 * n / (us * 1e-6) / 1e9)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (oracle on the host cores, bounded sample).
+# ---------------------------------------------------------------------------
+def cpu_baselines(rows=16384, hidden=4096) -> dict:
+    from oracle import fa as ofa
+    from oracle import rmsnorm as orms
+    from oracle import sana as osana
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+
+    def med(fn, reps):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    out = {}
+    g = _gen(1)
+    x = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    t = med(lambda: orms.rmsnorm(x, w, 1e-6), 5)
+    out["rmsnorm"] = dict(value=(2 * rows * hidden * 2 + hidden * 2) / t / 1e9, unit="GB/s", cores=cores,
+                          kind="port", seconds_per_pass=t,
+                          sample=f"oracle.rmsnorm on the full bf16 [{rows},{hidden}] input, median of 5")
+    qkv = torch.randn(2, 4096, 3, 70 * 32, generator=g).to(torch.bfloat16)
+    t = med(lambda: osana.linear_attention(qkv, 70, 32), 3)
+    out["sana"] = dict(value=4 * 2 * 70 * 4096 * 32 * 33 / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                       seconds_per_pass=t,
+                       sample="oracle.sana.linear_attention (fp32) on the full B=2,H=70,N=4096 input, median of 3")
+    # FA: one (batch, head) slice of B=2, H=16, N=4096, D=128 (1/32 of the work).
+    q, k, v, tq, tk, tv = (torch.randn(1, 4096, 1, 128, generator=g).to(torch.bfloat16) for _ in range(6))
+    t = med(lambda: ofa.attention_jvp(q, k, v, tq, tk, tv), 1)
+    flops = 12 * 4096 * 4096 * 128
+    out["fa"] = dict(value=flops / t / 1e12, unit="TFLOP/s", cores=cores, kind="port", seconds_per_pass=t,
+                     seconds_full_config_est=32 * t,
+                     sample="oracle.fa.attention_jvp (dense fp32 torch.func.jvp) on 1 of the 32 (b,h) "
+                            "slices of B=2,H=16,N=4096,D=128, median of 1 after 1 warm-up")
+    return out
+
+
+def load_traffic() -> dict:
+    """Per-kernel HBM bytes per dispatch measured with rocprofv3 --pmc (committed under profiles/)."""
+    path = ROOT / "profiles" / "traffic.json"
+    if path.exists():
+        try:
+            return json.loads(path.read_text())
+        except ValueError:
+            return {}
+    return {}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default=None,
+                    help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|copy), e.g. under rocprofv3")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only; run with --gpus 1 (the hot paths are "
+              "single-GPU kernels; sharding is described in DESIGN.md)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+    torch.cuda.init()
+    steps, warmup = args.steps, args.warmup
+
+    runners = {
+        "rmsnorm2048": lambda: bench_rmsnorm(2048, steps, warmup),
+        "rmsnorm4096": lambda: bench_rmsnorm(4096, steps, warmup),
+        "rmsnorm8192": lambda: bench_rmsnorm(8192, steps, warmup),
+        "sanaA": lambda: bench_sana(2, 70, 4096, steps, warmup),
+        "sanaB": lambda: bench_sana(1, 70, 16384, steps, warmup),
+        "fa_fwd_jvp": lambda: bench_fa("fwd_jvp", max(5, steps // 10), max(2, warmup // 5)),
+        "fa_jvp": lambda: bench_fa("jvp", max(5, steps // 10), max(2, warmup // 5)),
+        "fa_fwd": lambda: bench_fa("fwd", max(5, steps // 10), max(2, warmup // 5)),
+        "copy": lambda: bench_copy(max(5, steps // 5), 3),
+    }
+    if args.only:
+        r = runners[args.only]()
+        print(json.dumps(r), flush=True)
+        return 0
+
+    results = {}
+    for name, fn in runners.items():
+        results[name] = fn()
+        print(f"# {name}: {results[name]['us']:.2f} us", file=sys.stderr, flush=True)
+    head = results["rmsnorm4096"]
+    traffic = load_traffic()
+    tr = traffic.get(head["kernel"] + ":" + head["workload"])
+    cpu = None if args.no_cpu else cpu_baselines()
+    for name in results:
+        if cpu and name.startswith("rmsnorm") and name == "rmsnorm4096":
+            results[name]["speedup_vs_cpu"] = head["gbs"] / cpu["rmsnorm"]["value"]
+        if cpu and name.startswith("sana"):
+            results[name]["speedup_vs_cpu_sanaA_oracle"] = results[name]["tflops"] / cpu["sana"]["value"]
+        if cpu and name.startswith("fa_"):
+            results[name]["speedup_vs_cpu"] = results[name]["tflops"] / cpu["fa"]["value"]
+        t = traffic.get(results[name]["kernel"] + ":" + results[name]["workload"])
+        if t is not None:
+            results[name]["traffic_bytes"] = t
+    line = {
+        "metric": BASELINE_METRIC,
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": head["us"] / 1000.0,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": head["workload"], "rows": 16384, "hidden": 4096, "eps": 1e-6,
+                   "input_sets_rotated": head["sets"]},
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": tr,
+                     "algorithmic_bytes": head["bytes"], "kernel": head["kernel"]},
+        "cpu_baseline": None if cpu is None else {
+            "value": round(cpu["rmsnorm"]["value"], 3), "unit": "GB/s", "cores": cpu["rmsnorm"]["cores"],
+            "kind": "port", "sample": cpu["rmsnorm"]["sample"]},
+        "results": results,
+        "cpu_baselines": cpu,
+        "copy_ceiling_gbs": round(results["copy"]["gbs"], 1),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
