@@ -1,0 +1,84 @@
+"""CPU tests of the Python host layer: argument validation with the reference's
+message fragments (flash_attention_jvp/test.py:194-209; SANA_LinearAttention/
+custom.py:350-353; rmsnorm factory dtypes), no GPU needed and no CPU fallback
+(CPU tensors are rejected, never computed)."""
+
+import pytest
+import torch
+
+from kernelforge_amd.flash_attention_jvp import custom as fa
+from kernelforge_amd.rmsnorm import custom_rms_norm, rms_norm_tensor
+from kernelforge_amd.SANA_LinearAttention import qkv_attn_matmul
+
+
+def qkv(b=1, nq=9, nk=13, h=2, hk=2, d=64, dtype=torch.float16):
+    return (torch.zeros(b, nq, h, d, dtype=dtype), torch.zeros(b, nk, hk, d, dtype=dtype),
+            torch.zeros(b, nk, hk, d, dtype=dtype))
+
+
+def test_fa_validation_messages():
+    q, k, v = qkv()
+    with pytest.raises(ValueError, match="finite"):
+        fa._validate_inputs(q, k, v, float("nan"))
+    with pytest.raises(ValueError, match="positive"):
+        fa._validate_inputs(q, k, v, 0.0)
+    with pytest.raises(ValueError, match="float16"):
+        fa._validate_inputs(q.float(), k.float(), v.float(), None)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        fa._validate_inputs(*qkv(d=12), None)
+    with pytest.raises(ValueError, match="divisible"):
+        fa._validate_inputs(*qkv(h=3, hk=2), None)
+    with pytest.raises(ValueError, match="shape"):
+        fa._validate_inputs(q[0], k, v, None)
+    with pytest.raises(ValueError, match="CUDA"):
+        fa._validate_inputs(q, k, v, None)  # valid but on the CPU: rejected, never computed
+    with pytest.raises(ValueError, match="tq"):
+        fa._prepare_tangent(q[:, :-1], q, "tq")
+    assert fa._prepare_tangent(None, q, "tq") is None
+
+
+def test_fa_cpu_tensors_are_rejected_not_computed():
+    q, k, v = qkv()
+    with pytest.raises(ValueError, match="CUDA"):
+        fa.flash_attention(q, k, v)
+    with pytest.raises(ValueError, match="CUDA"):
+        fa.flash_attention_fwd_jvp(q, k, v, None, None, None)
+
+
+def test_sana_factory_validation():
+    with pytest.raises(ValueError, match="dim"):
+        qkv_attn_matmul(1, 2, 48, 16)
+    with pytest.raises(ValueError, match="dim"):
+        qkv_attn_matmul(1, 2, 256, 16)
+    with pytest.raises(ValueError, match="output_dtype"):
+        qkv_attn_matmul(1, 2, 32, 16, output_dtype="float64")
+    run = qkv_attn_matmul(1, 2, 32, 16, dtype="bfloat16")
+    with pytest.raises(ValueError):
+        run(torch.zeros(1, 16, 3, 64, dtype=torch.float16))
+    with pytest.raises(ValueError, match="device"):
+        run(torch.zeros(1, 16, 3, 64, dtype=torch.bfloat16))
+
+
+def test_rmsnorm_factory_validation():
+    with pytest.raises(ValueError, match="dtype"):
+        custom_rms_norm(1, 4, 64, 1e-6, "int8")
+    k = custom_rms_norm(1, 4, 64, 1e-6, "bfloat16")
+    with pytest.raises(ValueError):
+        k(torch.zeros(1, 4, 32, dtype=torch.bfloat16), torch.ones(32, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="device"):
+        k(torch.zeros(1, 4, 64, dtype=torch.bfloat16), torch.ones(64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="device"):
+        rms_norm_tensor(torch.zeros(3, 8), torch.ones(8))
+
+
+def test_fake_impls_for_tracing():
+    """The custom ops carry fake implementations (shape inference without a device)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        q = torch.empty(1, 9, 2, 64, dtype=torch.bfloat16)
+        k = torch.empty(1, 13, 2, 64, dtype=torch.bfloat16)
+        out, lse = fa._fwd_fake(q, k, k, 0.1, False)
+        assert out.shape == q.shape and lse.shape == (1, 2, 9) and lse.dtype == torch.float32
+        o, l2, t = fa._fwd_jvp_fake(q, k, k, None, None, None, 0.1, True)
+        assert t.shape == q.shape

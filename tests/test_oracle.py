@@ -1,0 +1,217 @@
+"""CPU tests that pin the oracle (no GPU).
+
+Each oracle function is checked against the golden fixtures (pure-Python fp64
+brute force with a different algorithm, tests/golden/make_golden.py) and
+against what the mathematics fixes: closed forms, invariants, finite
+differences.  The `test_mutation_*` tests plant a plausible mistake in a copy
+of an oracle function and assert that the corresponding check fails, i.e.
+that the check actually pins something.
+"""
+
+import json
+import math
+from pathlib import Path
+
+import pytest
+import torch
+
+from oracle import fa as ofa
+from oracle import rmsnorm as orms
+from oracle import sana as osana
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load(name):
+    return json.loads((GOLDEN / f"{name}_golden.json").read_text())
+
+
+def t64(x):
+    return torch.tensor(x, dtype=torch.float64)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", load("rmsnorm"), ids=lambda c: f"{c['rows']}x{c['dim']}")
+def test_rmsnorm_golden(case):
+    x, w, y = t64(case["x"]), t64(case["w"]), t64(case["y"])
+    torch.testing.assert_close(orms.rmsnorm_fp64(x, w, case["eps"]), y, rtol=1e-12, atol=0)
+    out32 = orms.rmsnorm(x.float(), w.float(), case["eps"])
+    torch.testing.assert_close(out32.double(), y, rtol=3e-7, atol=1e-30)
+    outbf = orms.rmsnorm(x.bfloat16(), w.bfloat16(), case["eps"])
+    # two bf16 roundings: |err| <= 2^-8 |y| * (1 + |w|) roughly; use 2 ulps
+    assert ((outbf.double() - y).abs() <= 2.0 ** -7 * y.abs() + 1e-12).all()
+
+
+def test_rmsnorm_unit_rms_and_scale_equivariance():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(16, 300, generator=g, dtype=torch.float64)
+    y = orms.rmsnorm_fp64(x, torch.ones(300, dtype=torch.float64), 0.0)
+    torch.testing.assert_close(y.pow(2).mean(-1).sqrt(), torch.ones(16, dtype=torch.float64))
+    torch.testing.assert_close(orms.rmsnorm_fp64(7.5 * x, torch.ones(300, dtype=torch.float64), 0.0), y)
+    # eps only matters relative to the mean square
+    a = orms.rmsnorm_noweight(x.float(), 1e-12)
+    torch.testing.assert_close(a.double(), y, rtol=1e-6, atol=1e-7)
+
+
+def test_mutation_rmsnorm_mean_vs_sum():
+    case = load("rmsnorm")[0]
+    x, w, y = t64(case["x"]), t64(case["w"]), t64(case["y"])
+    bad = x / torch.sqrt(x.pow(2).sum(-1, keepdim=True) + case["eps"]) * w  # sum instead of mean
+    assert not torch.allclose(bad, y, rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# SANA linear attention
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("case", load("sana"), ids=lambda c: f"B{c['B']}N{c['N']}H{c['H']}D{c['D']}")
+def test_sana_golden(case):
+    qkv, ref = t64(case["qkv"]), t64(case["out"])
+    H, D = case["H"], case["D"]
+    out = osana.linear_attention(qkv.float(), H, D, case["eps"])
+    torch.testing.assert_close(out.double(), ref, rtol=1e-5, atol=1e-6)
+    for splits in (1, 2, 3, case["N"]):
+        torch.testing.assert_close(osana.linear_attention_split(qkv, H, D, splits, case["eps"]), ref,
+                                   rtol=1e-10, atol=1e-12)
+
+
+def test_sana_invariants():
+    g = torch.Generator().manual_seed(1)
+    qkv = torch.randn(2, 50, 3, 4 * 8, generator=g, dtype=torch.float64)
+    out = osana.linear_attention(qkv, 4, 8)
+    # linear in v
+    q2 = qkv.clone()
+    q2[:, :, 2] *= -3.0
+    torch.testing.assert_close(osana.linear_attention(q2, 4, 8), -3.0 * out)
+    # relu(q) = 0 -> 0
+    q3 = qkv.clone()
+    q3[:, :, 0] = -q3[:, :, 0].abs()
+    assert torch.count_nonzero(osana.linear_attention(q3, 4, 8)) == 0
+    # v = const -> out = const wherever the denominator is non-zero
+    q4 = qkv.clone()
+    q4[:, :, 2] = 2.5
+    o4 = osana.linear_attention(q4, 4, 8)
+    # (rows whose relu(q) is all zero for a head have a zero denominator -> 0)
+    live = (torch.relu(qkv[:, :, 0]).reshape(2, 50, 4, 8).sum(-1) > 0).repeat_interleave(8, dim=-1)
+    torch.testing.assert_close(o4[live], torch.full_like(o4[live], 2.5))
+    assert torch.count_nonzero(o4[~live]) == 0
+
+
+def test_sana_eager_bf16_close_to_fp32():
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(1, 256, 3, 2 * 32, generator=g).bfloat16()
+    a = osana.linear_attention(qkv, 2, 32, fp32_attention=True)
+    b = osana.linear_attention(qkv, 2, 32, fp32_attention=False)
+    torch.testing.assert_close(b, a, atol=2e-2, rtol=2e-2)
+
+
+def test_mutation_sana_drop_ones_row_or_transpose():
+    case = load("sana")[0]
+    qkv, ref = t64(case["qkv"]), t64(case["out"])
+    H, D = case["H"], case["D"]
+    q, k, v = osana.unpack_qkv(qkv, H, D)
+    q, k = torch.relu(q), torch.relu(k)
+    # a PAD_VAL of 0 (dropped denominator) is caught
+    vk = torch.nn.functional.pad(v, (0, 0, 0, 1), value=0.0) @ k
+    out = vk @ q
+    bad = (out[:, :, :-1] / (out[:, :, -1:] + 1e-15)).reshape(case["B"], H * D, -1).permute(0, 2, 1)
+    assert not torch.allclose(bad, ref, rtol=1e-3)
+    # a transposed state (S^T instead of S) is caught
+    vk = torch.nn.functional.pad(v, (0, 0, 0, 1), value=1.0) @ k
+    st = torch.cat([vk[:, :, :-1].transpose(-1, -2), vk[:, :, -1:]], dim=2)
+    out = st @ q
+    bad = (out[:, :, :-1] / (out[:, :, -1:] + 1e-15)).reshape(case["B"], H * D, -1).permute(0, 2, 1)
+    assert not torch.allclose(bad, ref, rtol=1e-3)
+
+
+# ---------------------------------------------------------------------------
+# FlashAttention forward / JVP
+# ---------------------------------------------------------------------------
+def _fa_tensors(case):
+    def t(name):
+        return t64(case[name])  # [B, S, H, D]
+    return tuple(t(n) for n in ("q", "k", "v", "tq", "tk", "tv"))
+
+
+FA_CASES = load("fa")
+
+
+@pytest.mark.parametrize("case", FA_CASES, ids=lambda c: f"{c['Nq']}x{c['Nk']}H{c['Hq']}/{c['Hkv']}D{c['D']}c{int(c['causal'])}")
+def test_fa_golden(case):
+    q, k, v, tq, tk, tv = _fa_tensors(case)
+    kw = dict(softmax_scale=case["scale"], causal=case["causal"])
+    out, tout = ofa.attention_jvp(q, k, v, tq, tk, tv, **kw)
+    torch.testing.assert_close(out, t64(case["out"]), rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(tout, t64(case["tout"]), rtol=1e-10, atol=1e-12)
+    lse = ofa.attention_lse(q, k, **kw)
+    torch.testing.assert_close(lse, t64(case["lse"]), rtol=1e-12, atol=1e-12)
+    dense = ofa.attention_jvp_from_forward(q, k, v, tq, tk, tv, out, lse, **kw)
+    torch.testing.assert_close(dense.double(), t64(case["tout"]), rtol=1e-5, atol=1e-6)
+    for bn in (1, 2, 3, 64):
+        o2, l2, t2 = ofa.fused_forward_jvp_tiled(q, k, v, tq, tk, tv, block_n=bn, **kw)
+        torch.testing.assert_close(o2, t64(case["out"]), rtol=1e-10, atol=1e-12)
+        torch.testing.assert_close(t2, t64(case["tout"]), rtol=1e-10, atol=1e-12)
+        torch.testing.assert_close(l2, t64(case["lse"]), rtol=1e-12, atol=1e-12)
+
+
+def _rand(shape, seed):
+    return torch.randn(shape, generator=torch.Generator().manual_seed(seed), dtype=torch.float64)
+
+
+@pytest.mark.parametrize("causal", (False, True))
+def test_fa_finite_difference_and_tiled(causal):
+    B, Nq, Nk, Hq, Hkv, D = 1, 9, 13, 4, 2, 16
+    q, tq = _rand((B, Nq, Hq, D), 1), _rand((B, Nq, Hq, D), 2)
+    k, v, tk, tv = (_rand((B, Nk, Hkv, D), s) for s in (3, 4, 5, 6))
+    _, tout = ofa.attention_jvp(q, k, v, tq, tk, tv, causal=causal)
+    eps = 1e-5
+    plus = ofa.attention(q + eps * tq, k + eps * tk, v + eps * tv, causal=causal)
+    minus = ofa.attention(q - eps * tq, k - eps * tk, v - eps * tv, causal=causal)
+    torch.testing.assert_close(tout, (plus - minus) / (2 * eps), rtol=1e-6, atol=1e-8)
+    for bn in (4, 5, 16):
+        o, lse, t = ofa.fused_forward_jvp_tiled(q, k, v, tq, tk, tv, causal=causal, block_n=bn)
+        torch.testing.assert_close(t, tout, rtol=1e-10, atol=1e-12)
+
+
+def test_fa_consistency_checks():
+    """Derivation section 11: uniform shift -> 0, value-only -> P tv, mass preservation."""
+    B, N, H, D = 1, 11, 2, 8
+    q, k, v, tv = (_rand((B, N, H, D), s) for s in (7, 8, 9, 10))
+    zero = torch.zeros_like(q)
+    _, t = ofa.attention_jvp(q, k, v, None, torch.ones_like(k) * 0.25, None)
+    assert t.abs().max() < 1e-12
+    out, t = ofa.attention_jvp(q, k, v, None, None, tv)
+    torch.testing.assert_close(t, ofa.attention(q, k, tv))
+    # mass preservation: with v = 1 the output is 1 for every tangent, so tO = 0
+    ones = torch.ones_like(v)
+    _, t = ofa.attention_jvp(q, k, ones, _rand(q.shape, 11), _rand(k.shape, 12), zero[:, :, :, :] * 0)
+    assert t.abs().max() < 1e-12
+
+
+def test_mutation_fa_wrong_sign_or_missing_correction():
+    case = FA_CASES[0]
+    q, k, v, tq, tk, tv = _fa_tensors(case)
+    gamma = case["D"] ** -0.5
+    qh, kh, vh, tqh, tkh, tvh = (x.transpose(1, 2) for x in (q, k, v, tq, tk, tv))
+    grp = case["Hq"] // case["Hkv"]
+    kh, vh, tkh, tvh = (x.repeat_interleave(grp, dim=1) for x in (kh, vh, tkh, tvh))
+    p = (qh @ kh.transpose(-1, -2) * gamma).softmax(-1)
+    ts = (tqh @ kh.transpose(-1, -2) + qh @ tkh.transpose(-1, -2)) * gamma
+    ref = t64(case["tout"]).transpose(1, 2)
+    missing = p @ tvh + (p * ts) @ vh  # no "- rowsum(H) O" term
+    assert not torch.allclose(missing, ref, atol=1e-3)
+    flipped = p @ tvh + (p * ts) @ vh + (p * ts).sum(-1, keepdim=True) * (p @ vh)
+    assert not torch.allclose(flipped, ref, atol=1e-3)
+    good = p @ tvh + (p * ts) @ vh - (p * ts).sum(-1, keepdim=True) * (p @ vh)
+    torch.testing.assert_close(good, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_fa_empty_rows_convention():
+    case = FA_CASES[2]  # Nq=5 > Nk=3 causal: rows 0..1 have no valid key
+    q, k, v, tq, tk, tv = _fa_tensors(case)
+    out, t = ofa.attention_jvp(q, k, v, tq, tk, tv, causal=True, softmax_scale=case["scale"])
+    assert torch.count_nonzero(out[:, :2]) == 0 and torch.count_nonzero(t[:, :2]) == 0
+    lse = ofa.attention_lse(q, k, causal=True, softmax_scale=case["scale"])
+    assert torch.isinf(lse[:, :, :2]).all() and (lse[:, :, :2] > 0).all()
+    assert math.isinf(case["lse"][0][0][0])
