@@ -4,8 +4,8 @@
 // its forward-mode derivative, and the single-pass online recurrence of
 // flash_attention_jvp/flash-attention-jvp-derivation.md:388-558:
 //   S = scale q k^T, tS = scale (tq k^T + q tk^T), E = exp(S - m),
-//   l = a l + rowsum(E), U = a U + E v, r = a r + rowsum(E*tS),
-//   G = a G + (E*tS) v + E tv;   O = U/l, tO = G/l - (r/l) O, LSE = m + log l.
+//   l = sum E, U = E v, r = sum E*tS, G = (E*tS) v + E tv;
+//   O = U/l, tO = G/l - (r/l) O, LSE = m + log l.
 // The JVP-from-LSE mode recomputes P = exp(S - LSE) (flash_attention_jvp/
 // custom.py:88-118) and, unlike the reference, does not use the cached 16-bit
 // O in tO = P tv + H v - rowsum(H) O: that term multiplies O's rounding error
@@ -13,26 +13,28 @@
 // U = P v alongside (one more product) and normalises like the fused mode:
 //   tO = (P tv + H v)/l - (rowsum(H)/l) (U/l),  l = rowsum(P) of the rounded P.
 //
-// Tiling.  A workgroup is 4 wavefronts x 32 query rows (128 rows) of one
-// (batch, head); it scans the key axis in tiles of 64 keys.  Per tile each
-// wavefront computes the transposed score block S^T = K Q^T with
-// v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q held in registers), so lane
-// l owns query row l%32 and 16 keys per 32-key block.  That makes every row
-// statistic (max, l, r, the rescale factor) lane-local, and the score
-// registers are already the B operand of the next product O^T += V^T E^T once
-// the keys are enumerated in the order the accumulator holds them:
-// k = 8*(j/4) + 4*(l/32) + j%4 for operand element j.  V^T is read from the
-// row-major V tile with ds_read_b64_tr_b16 in that same key order.
+// Tiling.  A workgroup is 8 wavefronts x 16 query rows (128 rows) of one
+// (batch, head), two wavefronts per SIMD so that one wavefront's softmax
+// arithmetic runs while the other's matrix products occupy the MFMA pipe.  It
+// scans the key axis in tiles of 64 keys.  Per tile each wavefront computes
+// the transposed score blocks S^T = K Q^T with v_mfma_f32_16x16x32 (A = K rows
+// from LDS, B = Q held in registers): lane l owns query row l%16 and keys
+// 16*kb + 4*(l/16) + i of key block kb.  Those accumulators are directly the
+// B operand of O^T += V^T E^T once the K index of each 32-key step is
+// enumerated as (keys 4*(l/16)+0..3 of block 2kk, then of block 2kk+1); V^T
+// is read from the row-major V tile with ds_read_b64_tr_b16 in that order.
 //
 // Memory.  K, V (and tK, tV) tiles stream HBM -> LDS with global_load_lds
 // (16 B per lane, no VGPR staging), double buffered, rows XOR-swizzled in
-// 16-byte chunks so both the row reads (ds_read_b128) and the transposing
-// reads are free of bank conflicts.  Workgroups are renumbered so that all
-// query tiles of one head run on one XCD and share its L2.
+// 16-byte chunks so that neither the row reads (ds_read_b128) nor the
+// transposing reads (ds_read_b64_tr_b16) conflict in the LDS banks.  Workgroups are renumbered so that all query tiles of one head run
+// on one XCD and share its L2.
 //
-// The running max is only raised when a tile's max exceeds it by more than
-// 2^8 (log2 units); E then stays <= 256 and O = U/l, LSE = m + log l remain
-// exact because U, l, r, G all use the same reference.
+// Exponent reference.  FWD/FWD_JVP fix each row's reference m at the max of
+// its first key tile and never raise it, so U and G are never rescaled inside
+// the scan.  A later score exceeding m by ~2^7 (log2 units; 2^4 for fp16 E)
+// overflows to a non-finite accumulator, which the workgroup detects at the
+// end and answers by redoing its rows with a lazily rescaling scan.
 #include <type_traits>
 
 #include "kf_common.h"
@@ -44,10 +46,11 @@ enum FaMode { FA_FWD = 0, FA_FWD_JVP = 1, FA_JVP = 2 };
 
 constexpr int kBQ = 128;   // query rows per workgroup
 constexpr int kBK = 64;    // keys per tile
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;  // wavefronts per workgroup (16 query rows each)
+constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr float kRescaleThreshold = 8.0f;
+constexpr float kRescaleThreshold = 8.0f;  // lazy rescale step of the rescaling scan (log2)
 
 // 256 bytes of zeros in global memory: the source of lanes whose chunk is
 // outside the tensor (key rows >= Nk, head-dim padding).
@@ -69,27 +72,71 @@ struct FaParams {
     int causal;
 };
 
-template <int CH> __device__ __forceinline__ int swz(int row) {
-    return (2 * (row & 3) + ((row >> 2) & 1)) & (CH - 1);
+// Physical 16-byte chunk = logical chunk ^ swz(row), for CH chunks per row.
+// Chosen (by enumerating the XOR-linear maps of row % 16 and checking them
+// against measured LDS conflict counts) so that neither the ds_read_b128 of a
+// K block (16 consecutive rows at one logical chunk) nor the
+// ds_read_b64_tr_b16 of a V^T operand (8 consecutive rows x an aligned pair of
+// chunks) has bank conflicts; swz depends on row % 16 only.
+template <int CH> __device__ __forceinline__ int swz(int r) {
+    if constexpr (CH == 16) return (r & 15) ^ ((r & 1) * 12);
+    else if constexpr (CH == 8) return (r & 7) ^ ((r & 1) << 2);
+    else return ((r >> 1) & 1) | ((((r >> 1) ^ (r >> 2)) & 1) << 1);
 }
 
-// Async copy of one [kBK][DP] tile (keys k0.., one kv head) into LDS.
+// Async copy of one [kBK][DP] tile (keys k0.., one kv head) into LDS.  A tile
+// is CH = DP/8 copy instructions of 64 lanes x 16 B; wavefront w issues
+// instructions w, w + kWaves, ...
 template <typename T, int DP>
 __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_stride, int keys_valid,
                                           int D, int wave, int lane) {
     constexpr int CH = DP / 8;
     constexpr int RPI = 64 / CH;
-    constexpr int NI = kBK / (RPI * kWaves);
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        const int row0 = (i * kWaves + wave) * RPI;
-        const int row = row0 + lane / CH;
-        const int chunk = (lane % CH) ^ swz<CH>(row);
-        const void* src = (row < keys_valid && chunk * 8 < D)
-                               ? static_cast<const void*>(g + row * row_stride + chunk * 8)
-                               : static_cast<const void*>(g_zero16);
-        __builtin_amdgcn_global_load_lds(
-            src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+    for (int j = 0; j < (CH + kWaves - 1) / kWaves; ++j) {
+        const int i = wave + j * kWaves;
+        if (CH % kWaves == 0 || i < CH) {
+            const int row0 = i * RPI;
+            const int row = row0 + lane / CH;
+            const int chunk = (lane % CH) ^ swz<CH>(row);
+            const void* src = (row < keys_valid && chunk * 8 < D)
+                                   ? static_cast<const void*>(g + row * row_stride + chunk * 8)
+                                   : static_cast<const void*>(g_zero16);
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+        }
+    }
+}
+
+// Byte offset, within a full tile, of the 16-byte chunk lane `lane` copies.
+// The rows a lane copies are wave*RPI + lane/CH plus multiples of
+// kWaves*RPI >= 16, so their swizzle (a function of row % 16) is the same for
+// every instruction and one offset serves them all.
+template <typename T, int DP>
+__device__ __forceinline__ uint32_t full_tile_lane_offset(int64_t row_stride, int wave, int lane) {
+    constexpr int CH = DP / 8;
+    constexpr int RPI = 64 / CH;
+    const int row = wave * RPI + lane / CH;
+    const int chunk = (lane % CH) ^ swz<CH>(row);
+    return (uint32_t)(((int64_t)(lane / CH) * row_stride + chunk * 8) * (int64_t)sizeof(T));
+}
+
+// Async copy of a tile whose 64 rows are all valid and whose rows hold exactly
+// DP elements: a uniform base per instruction plus one per-lane offset.
+template <typename T, int DP>
+__device__ __forceinline__ void load_tile_full(T* tile, const T* g, int64_t row_stride, uint32_t voff,
+                                               int wave) {
+    constexpr int CH = DP / 8;
+    constexpr int RPI = 64 / CH;
+#pragma unroll
+    for (int j = 0; j < (CH + kWaves - 1) / kWaves; ++j) {
+        const int i = wave + j * kWaves;
+        if (CH % kWaves == 0 || i < CH) {
+            const int row0 = i * RPI;
+            const char* src = reinterpret_cast<const char*>(g + (int64_t)row0 * row_stride) + voff;
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+        }
     }
 }
 
@@ -106,15 +153,18 @@ __device__ __forceinline__ const T* tr_addr(const T* tile, int row, int d) {
     return tile + row * DP + (((d >> 3) ^ swz<DP / 8>(row)) << 3) + (d & 7);
 }
 
-// A operand V^T[d][k] for K-step ks2 (keys 16*ks2..) of d-block db, keys in
-// accumulator order.
+// A operand V^T[d][k] of the 32-key step kk and 16-wide d block db: lane l
+// (g = l/16) holds d = 16*db + l%16 and keys 32*kk + 4*g + 0..3 (elements
+// 0..3) and 32*kk + 16 + 4*g + 0..3 (elements 4..7).  In ds_read_b64_tr_b16
+// lanes 4q..4q+3 of each 16-lane group address row q's 16 elements; lane j of
+// the group then receives element j of rows 0..3.
 template <typename T, int DP>
-__device__ __forceinline__ typename V<T>::x8 vt_operand(const T* tile, int ks2, int db, int lane) {
-    const int G = lane >> 4, j16 = lane & 15;
-    const int row = 16 * ks2 + 4 * (G >> 1) + (j16 >> 2);
-    const int d = 32 * db + 16 * (G & 1) + 4 * (j16 & 3);
+__device__ __forceinline__ typename V<T>::x8 vt_operand(const T* tile, int kk, int db, int lane) {
+    const int g = lane >> 4, j16 = lane & 15;
+    const int row = 32 * kk + 4 * g + (j16 >> 2);
+    const int d = 16 * db + 4 * (j16 & 3);
     const typename V<T>::x4 lo = lds_read_tr(tr_addr<T, DP>(tile, row, d));
-    const typename V<T>::x4 hi = lds_read_tr(tr_addr<T, DP>(tile, row + 8, d));
+    const typename V<T>::x4 hi = lds_read_tr(tr_addr<T, DP>(tile, row + 16, d));
     typename V<T>::x8 r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -126,17 +176,69 @@ __device__ __forceinline__ typename V<T>::x8 vt_operand(const T* tile, int ks2, 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Packed 16-bit pairs: round-to-nearest-even conversion of two floats and a
+// two-term fp32 dot product with (1, 1), used to sum the rounded values.
+template <typename T> struct Pk;
+template <> struct Pk<bf16> {
+    typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ unsigned cvt(float a, float b) {
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(unsigned, __builtin_convertvector(v, x2));
+    }
+    static __device__ __forceinline__ float sum_into(unsigned pk, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(x2, pk),
+                                               __builtin_bit_cast(x2, 0x3f803f80u), acc, false);
+    }
+};
+template <> struct Pk<f16> {
+    typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ unsigned cvt(float a, float b) {
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(unsigned, __builtin_convertvector(v, x2));
+    }
+    static __device__ __forceinline__ float sum_into(unsigned pk, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(x2, pk), __builtin_bit_cast(x2, 0x3c003c00u),
+                                      acc, false);
+    }
+};
+
+// Wait until this thread's global->LDS copies have landed (vmcnt = 0); the
+// LDS and scalar counters are left alone.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Reduce x over the four lanes l%16 + 16*g (g = 0..3) that share a query row.
+// v_permlane16_swap / v_permlane32_swap exchange the odd 16-lane (32-lane)
+// groups of their first operand with the even groups of the second; with both
+// operands x, op(r0, r1) combines each lane with its partner in the same
+// operand order in every lane, so all four lanes end with the same value.
+__device__ __forceinline__ float row_sum4(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_max4(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <typename T, int DP, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fa_kernel(const FaParams p) {
     constexpr bool JVP = MODE != FA_FWD;
-    constexpr int NT = JVP ? 4 : 2;          // tiles per stage: K, V (, tK, tV)
-    constexpr int KS = DP / 16;               // K-steps over the head dim
-    constexpr int DB = DP / 32;               // 32-wide d blocks of the output
-    __shared__ __attribute__((aligned(16))) T smem[2][NT][kBK * DP];
+    constexpr int NT = JVP ? 2 : 1;   // tensors per side: K (, tK) and V (, tV)
+    constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
+    constexpr int DB = DP / 16;        // 16-wide d blocks of the outputs
+    typedef typename V<T>::x8 x8;
+    __shared__ __attribute__((aligned(16))) T kside[2][NT][kBK * DP];
+    __shared__ __attribute__((aligned(16))) T vside[2][NT][kBK * DP];
+    __shared__ int bail_vote[kWaves];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int h = lane >> 5;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 4;  // 16-lane group: key sub-range / d sub-range
 
     // XCD-aware renumbering: hardware sends block i to XCD i % 8; give each XCD
     // a contiguous range of logical blocks (consecutive query tiles of a head).
@@ -149,8 +251,8 @@ void fa_kernel(const FaParams p) {
     if (p.causal) qtile = p.n_qtiles - 1 - qtile;  // longest scans first
     const int hk = hq / p.group;
 
-    const int q0w = qtile * kBQ + wave * 32;     // first row of this wavefront
-    const int qr = q0w + (lane & 31);            // this lane's query row
+    const int q0w = qtile * kBQ + wave * 16;     // first row of this wavefront
+    const int qr = q0w + (lane & 15);            // this lane's query row
     const bool row_ok = qr < p.Nq;
     const int64_t q_row_stride = (int64_t)p.Hq * p.D;
     const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
@@ -162,231 +264,320 @@ void fa_kernel(const FaParams p) {
     const bool has_tk = JVP && p.tk != nullptr;
     const bool has_tv = JVP && p.tv != nullptr;
 
-    // Q (and tQ) as B operands: lane l holds row qr, d = 16*ks + 8*h + 0..7.
-    typename V<T>::x8 qreg[KS], tqreg[KS];
+    // Q (and tQ) as B operands: lane l holds row qr, d = 32*ds + 8*grp + 0..7.
+    x8 qreg[DS], tqreg[DS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int d = 16 * ks + 8 * h;
+    for (int ds = 0; ds < DS; ++ds) {
+        const int d = 32 * ds + 8 * grp;
         const bool ok = row_ok && d < p.D;
-        u32x4 z = {0u, 0u, 0u, 0u};
-        u32x4 a = ok ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.q) + q_off + d) : z;
-        qreg[ks] = __builtin_bit_cast(typename V<T>::x8, a);
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        const u32x4 a = ok ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.q) + q_off + d) : z;
+        qreg[ds] = __builtin_bit_cast(x8, a);
         if constexpr (JVP) {
-            u32x4 t = (ok && has_tq)
-                          ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.tq) + q_off + d)
-                          : z;
-            tqreg[ks] = __builtin_bit_cast(typename V<T>::x8, t);
+            const u32x4 t = (ok && has_tq)
+                                ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.tq) + q_off + d)
+                                : z;
+            tqreg[ds] = __builtin_bit_cast(x8, t);
         }
     }
 
-    float lse2 = 0.f;  // JVP mode: cached LSE in log2 units
+    // JVP mode: -LSE in log2 units is the exponent offset (+inf LSE -> P = 0).
+    float nref_lse = 0.f;
     if constexpr (MODE == FA_JVP) {
-        lse2 = row_ok ? p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : __builtin_inff();
+        nref_lse = row_ok ? -p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : -__builtin_inff();
     }
 
     // Key range of the workgroup.
     int key_stop = p.Nk;
     if (p.causal) key_stop = min(p.Nk, max(0, qtile * kBQ + kBQ + diag));
     const int ntiles = (key_stop + kBK - 1) / kBK;
+    const int klim = p.causal ? min(p.Nk - 1, qr + diag) : p.Nk - 1;
+    const float c = p.scale_log2;
 
-    f32x16 u[DB], g[DB];
+    // Row statistics (each lane holds a quarter of its row's keys).  l_run and
+    // r_run sum the 16-bit E and H values the products consume, so O is an
+    // exact convex combination of V rows and tO = sum_j H_j (v_j - O) / l;
+    // l_lse sums the fp32 E for the LSE output.  m_run is in log2 units.
+    struct Stats {
+        float m_run, l_run, r_run, l_lse;
+    };
+
+    // Full tiles (all 64 keys valid, D == DP) take the uniform-address copy.
+    const uint32_t voff = full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane);
+    const bool dense_rows = p.D == DP;
+    const T* const kbase = static_cast<const T*>(p.k) + kv_base;
+    const T* const vbase = static_cast<const T*>(p.v) + kv_base;
+    const T* const tkbase = JVP && has_tk ? static_cast<const T*>(p.tk) + kv_base : nullptr;
+    const T* const tvbase = JVP && has_tv ? static_cast<const T*>(p.tv) + kv_base : nullptr;
+    auto tile_masked = [&](int k0) {
+        return (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
+    };
+    auto apply_mask = [&](f32x4 (&s)[4], int k0) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            u[db][i] = 0.f;
-            g[db][i] = 0.f;
+            for (int i = 0; i < 4; ++i)
+                if (k0 + 16 * kb + 4 * grp + i > klim) s[kb][i] = -__builtin_inff();
+    };
+    auto row_max = [&](const f32x4 (&s)[4]) {
+        float mx = s[0][0];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][i]);
+        return row_max4(mx) * c;
+    };
+
+    // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
+    auto epilogue = [&](const f32x4 (&u)[DB], const f32x4 (&g)[DB], const Stats& st) {
+        const float l_tot = row_sum4(st.l_run);
+        const float r_tot = row_sum4(st.r_run);
+        const float l_lse_tot = row_sum4(st.l_lse);
+        T* orow = static_cast<T*>(p.o) + q_off;
+        T* torow = static_cast<T*>(p.to) + q_off;
+        const bool empty = !(l_tot > 0.f);
+        const float inv = empty ? 0.f : 1.f / l_tot;
+        const float rl = r_tot * inv;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + 4 * grp;
+            if (row_ok && d < p.D) {
+                typename V<T>::x4 ov, tv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float o = u[db][e] * inv;
+                    ov[e] = (T)o;
+                    if constexpr (JVP) tv[e] = (T)(g[db][e] * inv - rl * o);
+                }
+                if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
+                if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
+            }
         }
-    // l_run / r_run sum the 16-bit E and H the products consume; l_lse sums
-    // the fp32 E for the LSE output.
-    float m_run = -__builtin_inff(), l_run = 0.f, r_run = 0.f, l_lse = 0.f;
-
-    auto issue = [&](int tile_idx) {
-        const int buf = tile_idx & 1;
-        const int k0 = tile_idx * kBK;
-        const int kv = p.Nk - k0;
-        const int64_t off = kv_base + (int64_t)k0 * kv_row_stride;
-        load_tile<T, DP>(smem[buf][0], static_cast<const T*>(p.k) + off, kv_row_stride, kv, p.D, wave, lane);
-        load_tile<T, DP>(smem[buf][1], static_cast<const T*>(p.v) + off, kv_row_stride, kv, p.D, wave, lane);
-        if constexpr (JVP) {
-            if (has_tk)
-                load_tile<T, DP>(smem[buf][2], static_cast<const T*>(p.tk) + off, kv_row_stride, kv, p.D, wave, lane);
-            if (has_tv)
-                load_tile<T, DP>(smem[buf][3], static_cast<const T*>(p.tv) + off, kv_row_stride, kv, p.D, wave, lane);
+        if (MODE != FA_JVP && grp == 0 && row_ok) {
+            p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] =
+                empty ? __builtin_inff() : (st.m_run + log2f(l_lse_tot)) * kLn2;
         }
     };
 
-    if (ntiles > 0) issue(0);
-    // The tile loop is instantiated twice: branch-free when every tangent is
+    // The scan is instantiated twice: branch-free when every tangent is
     // present (the common case), and with per-tangent checks otherwise.
     auto scan = [&](auto all_tag) {
-    constexpr bool ALL = decltype(all_tag)::value;
-    const bool use_tq = ALL || has_tq, use_tk = ALL || has_tk, use_tv = ALL || has_tv;
-    for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();  // tile `it` resident; everyone is done with buffer buf^1
-        if (it + 1 < ntiles) issue(it + 1);
-        const T* Kt = smem[buf][0];
-        const T* Vt = smem[buf][1];
-        const T* tKt = smem[buf][2 % NT];
-        const T* tVt = smem[buf][3 % NT];
-        const int k0 = it * kBK;
+        constexpr bool ALL = decltype(all_tag)::value;
+        const bool use_tq = ALL || has_tq, use_tk = ALL || has_tk, use_tv = ALL || has_tv;
 
-        const bool need_mask = (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
-        const int klim = p.causal ? min(p.Nk - 1, qr + diag) : p.Nk - 1;
-
-        // The tile is consumed in two 32-key blocks, each run from scores to
-        // the P.V products before the next starts (halves the live registers).
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) {
-            // ---- scores S^T (and tS^T) ----
-            f32x16 s, ts;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                s[i] = 0.f;
-                ts[i] = 0.f;
-            }
-            const int krow = 32 * sub + (lane & 31);
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const typename V<T>::x8 ka = row_chunk<T, DP>(Kt, krow, 2 * ks + h);
-                s = mfma32x32x16(ka, qreg[ks], s);
-                if constexpr (JVP) {
-                    if (use_tq) ts = mfma32x32x16(ka, tqreg[ks], ts);
-                    if (use_tk) {
-                        const typename V<T>::x8 tka = row_chunk<T, DP>(tKt, krow, 2 * ks + h);
-                        ts = mfma32x32x16(tka, qreg[ks], ts);
-                    }
-                }
-            }
-
-            // ---- scale to log2 units; mask tiles crossing Nk or the diagonal ----
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float x = s[i] * p.scale_log2;
-                if (need_mask) {
-                    const int key = k0 + 32 * sub + 8 * (i >> 2) + 4 * h + (i & 3);
-                    if (key > klim) x = -__builtin_inff();
-                }
-                s[i] = x;
-            }
-
-            // ---- probabilities: E (online, FWD/FWD_JVP) or P (from LSE) ----
-            float ref;
-            if constexpr (MODE == FA_JVP) {
-                ref = lse2;
+        // Copies of one side of tile `tile` into its buffer: the K side (K,
+        // tK) or the V side (V, tV).  The two halves are issued at different
+        // points of the previous tile's work so that the wavefronts of a
+        // workgroup do not all queue their copies at the same moment.
+        auto issue_side = [&](int tile, bool vs) {
+            const int buf = tile & 1, k0 = tile * kBK;
+            const int64_t off = (int64_t)k0 * kv_row_stride;
+            T* const d0 = vs ? vside[buf][0] : kside[buf][0];
+            T* const d1 = vs ? vside[buf][NT - 1] : kside[buf][NT - 1];
+            const T* const s0 = (vs ? vbase : kbase) + off;
+            const T* const s1 = (vs ? tvbase : tkbase) + off;
+            const bool tan = JVP && (vs ? use_tv : use_tk);
+            if (dense_rows && k0 + kBK <= p.Nk) {
+                load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
+                if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
             } else {
-                float mx = -__builtin_inff();
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                const bool upd = mx > m_run + kRescaleThreshold;
-                if (__any(upd)) {
-                    // Rows that keep their reference use alpha = 1 (never
-                    // -inf - -inf); a row leaving m = -inf gets alpha = 0 on
-                    // its all-zero state.
-                    const float m_new = upd ? mx : m_run;
-                    const float alpha = upd ? fast_exp2(m_run - m_new) : 1.f;
-                    l_run *= alpha;
-                    l_lse *= alpha;
-#pragma unroll
-                    for (int db = 0; db < DB; ++db)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) u[db][i] *= alpha;
-                    if constexpr (JVP) {
-                        r_run *= alpha;
-#pragma unroll
-                        for (int db = 0; db < DB; ++db)
-#pragma unroll
-                            for (int i = 0; i < 16; ++i) g[db][i] *= alpha;
-                    }
-                    m_run = m_new;
-                }
-                ref = m_run == -__builtin_inff() ? 0.f : m_run;
+                const int kv = p.Nk - k0;
+                load_tile<T, DP>(d0, s0, kv_row_stride, kv, p.D, wave, lane);
+                if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
             }
+        };
+        auto issue = [&](int tile) {
+            issue_side(tile, false);
+            issue_side(tile, true);
+        };
 
-            // l and r accumulate the same 16-bit E and H values the products
-            // consume, so O is an exact convex combination of the V rows and
-            // tO = G - r O = sum_j H_j (v_j - O): the rounding of H_j is
-            // multiplied by (v_j - O), not by v_j (no cancellation blow-up).
-            typename V<T>::x8 eb[2], hb[2];
-            float lsum = 0.f, rsum = 0.f, esum = 0.f;
+        // S^T (and tS^T) of the 64 keys of the tile in buffer buf.
+        auto scores = [&](int buf, f32x4 (&s)[4], f32x4 (&ts)[4]) {
+            const T* Kt = kside[buf][0];
+            const T* tKt = kside[buf][NT - 1];
+            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float e = fast_exp2(s[i] - ref);
-                esum += e;
-                const T e16 = (T)e;
-                eb[i >> 3][i & 7] = e16;
-                lsum += (float)e16;
-                if constexpr (JVP) {
-                    const T h16 = (T)(e * (ts[i] * p.scale));
-                    hb[i >> 3][i & 7] = h16;
-                    rsum += (float)h16;
-                }
-            }
-            l_run += lsum;
-            r_run += rsum;
-            l_lse += esum;
-
-            // ---- O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T ----
+            for (int kb = 0; kb < 4; ++kb) {
+                s[kb] = zero;
+                ts[kb] = zero;
+                const int krow = 16 * kb + (lane & 15);
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const int ks2 = 2 * sub + kk;
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const typename V<T>::x8 va = vt_operand<T, DP>(Vt, ks2, db, lane);
-                    u[db] = mfma32x32x16(va, eb[kk], u[db]);
+                for (int ds = 0; ds < DS; ++ds) {
+                    const x8 ka = row_chunk<T, DP>(Kt, krow, 4 * ds + grp);
+                    s[kb] = mfma16x16x32(ka, qreg[ds], s[kb]);
                     if constexpr (JVP) {
-                        g[db] = mfma32x32x16(va, hb[kk], g[db]);
-                        if (use_tv) {
-                            const typename V<T>::x8 tva = vt_operand<T, DP>(tVt, ks2, db, lane);
-                            g[db] = mfma32x32x16(tva, eb[kk], g[db]);
+                        if (use_tq) ts[kb] = mfma16x16x32(ka, tqreg[ds], ts[kb]);
+                        if (use_tk) {
+                            const x8 tka = row_chunk<T, DP>(tKt, krow, 4 * ds + grp);
+                            ts[kb] = mfma16x16x32(tka, qreg[ds], ts[kb]);
                         }
                     }
                 }
             }
-        }
-    }
+        };
 
+        // E = exp2(S*c + nref) (or P for the JVP mode) and H = E * scale * tS,
+        // packed to 16 bits; their rounded values are summed into l and r.
+        auto probs = [&](const f32x4 (&s)[4], const f32x4 (&ts)[4], float nref, u32x2 (&ew)[4],
+                         u32x2 (&hw)[4], Stats& st) {
+            float esum = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float e0 = fast_exp2(fmaf(s[kb][2 * j], c, nref));
+                    const float e1 = fast_exp2(fmaf(s[kb][2 * j + 1], c, nref));
+                    if constexpr (MODE != FA_JVP) esum += e0 + e1;
+                    const unsigned pe = Pk<T>::cvt(e0, e1);
+                    ew[kb][j] = pe;
+                    st.l_run = Pk<T>::sum_into(pe, st.l_run);
+                    if constexpr (JVP) {
+                        const unsigned ph = Pk<T>::cvt(e0 * (ts[kb][2 * j] * p.scale),
+                                                       e1 * (ts[kb][2 * j + 1] * p.scale));
+                        hw[kb][j] = ph;
+                        st.r_run = Pk<T>::sum_into(ph, st.r_run);
+                    }
+                }
+            if constexpr (MODE != FA_JVP) st.l_lse += esum;
+        };
+
+        // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the tile in buffer buf.
+        auto pv = [&](f32x4 (&u)[DB], f32x4 (&g)[DB], int buf, const u32x2 (&ew)[4], const u32x2 (&hw)[4]) {
+            const T* Vt = vside[buf][0];
+            const T* tVt = vside[buf][NT - 1];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const x8 eb = __builtin_bit_cast(x8, u32x4{ew[2 * kk][0], ew[2 * kk][1], ew[2 * kk + 1][0],
+                                                           ew[2 * kk + 1][1]});
+                const x8 hb = __builtin_bit_cast(x8, u32x4{hw[2 * kk][0], hw[2 * kk][1], hw[2 * kk + 1][0],
+                                                           hw[2 * kk + 1][1]});
+#pragma unroll
+                for (int db = 0; db < DB; ++db) {
+                    const x8 va = vt_operand<T, DP>(Vt, kk, db, lane);
+                    u[db] = mfma16x16x32(va, eb, u[db]);
+                    if constexpr (JVP) {
+                        g[db] = mfma16x16x32(va, hb, g[db]);
+                        if (use_tv) {
+                            const x8 tva = vt_operand<T, DP>(tVt, kk, db, lane);
+                            g[db] = mfma16x16x32(tva, eb, g[db]);
+                        }
+                    }
+                }
+            }
+        };
+
+        auto zero_acc = [&](f32x4 (&acc)[DB]) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        };
+
+        // ---------------- fast scan: fixed exponent reference ----------------
+        {
+            f32x4 u[DB], g[DB];
+            zero_acc(u);
+            zero_acc(g);
+            Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
+            float nref = nref_lse;
+            f32x4 s[4], ts[4];
+            u32x2 ew[4], hw[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) hw[kb] = u32x2{0u, 0u};
+            if (ntiles > 0) issue(0);
+            for (int t = 0; t < ntiles; ++t) {
+                const int buf = t & 1, k0 = t * kBK;
+                wait_vmem();
+                __syncthreads();  // tile t resident; every wavefront is done with tile t-1
+                if (t + 1 < ntiles) issue_side(t + 1, false);
+                scores(buf, s, ts);
+                if (t + 1 < ntiles) issue_side(t + 1, true);
+                if (tile_masked(k0)) apply_mask(s, k0);
+                if constexpr (MODE != FA_JVP) {
+                    if (t == 0) {
+                        // Every non-empty row has a valid key in its first tile
+                        // (masks only cut keys off at the end).
+                        st.m_run = row_max(s);
+                        nref = st.m_run == -__builtin_inff() ? 0.f : -st.m_run;
+                    }
+                }
+                probs(s, ts, nref, ew, hw, st);
+                pv(u, g, buf, ew, hw);
+            }
+            if constexpr (MODE == FA_JVP) {
+                epilogue(u, g, st);
+                return;
+            } else {
+                // Overflow check, made uniform over the workgroup (the
+                // rescaling scan needs every wavefront for its tile copies).
+                bool fin = __builtin_isfinite(st.l_lse) && __builtin_isfinite(st.r_run);
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        fin = fin && __builtin_isfinite(u[db][i]);
+                        if constexpr (JVP) fin = fin && __builtin_isfinite(g[db][i]);
+                    }
+                const bool wave_bad = __any(!fin);
+                if (lane == 0) bail_vote[wave] = wave_bad;
+                __syncthreads();
+                int any_bad = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) any_bad |= bail_vote[w];
+                if (!any_bad) {
+                    epilogue(u, g, st);
+                    return;
+                }
+                wait_vmem();
+                __syncthreads();
+            }
+        }
+
+        // ---------------- rescaling scan (rare): one tile at a time ----------------
+        if constexpr (MODE != FA_JVP) {
+            f32x4 u[DB], g[DB];
+            zero_acc(u);
+            zero_acc(g);
+            Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
+            for (int t = 0; t < ntiles; ++t) {
+                const int buf = t & 1, k0 = t * kBK;
+                issue(t);
+                wait_vmem();
+                __syncthreads();
+                f32x4 s[4], ts[4];
+                u32x2 ew[4], hw[4] = {u32x2{0u, 0u}, u32x2{0u, 0u}, u32x2{0u, 0u}, u32x2{0u, 0u}};
+                scores(buf, s, ts);
+                if (tile_masked(k0)) apply_mask(s, k0);
+                // Raise the reference only when the max grew by more than 2^8:
+                // E stays <= 256.  A row leaving m = -inf gets alpha =
+                // exp2(-inf) = 0 on its all-zero state.
+                const float mx = row_max(s);
+                const bool upd = mx > st.m_run + kRescaleThreshold;
+                const float alpha = upd ? fast_exp2(st.m_run - mx) : 1.f;
+                if (upd) {
+                    st.m_run = mx;
+                    st.l_run *= alpha;
+                    st.r_run *= alpha;
+                    st.l_lse *= alpha;
+                }
+                if (__any(upd)) {
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            u[db][i] *= alpha;
+                            g[db][i] *= alpha;
+                        }
+                }
+                probs(s, ts, st.m_run == -__builtin_inff() ? 0.f : -st.m_run, ew, hw, st);
+                pv(u, g, buf, ew, hw);
+                __syncthreads();
+            }
+            epilogue(u, g, st);
+        }
     };
     if (!JVP || (has_tq && has_tk && has_tv))
         scan(std::true_type{});
     else
         scan(std::false_type{});
-
-    // ---- epilogue ----
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float r_tot = r_run + __shfl_xor(r_run, 32, 64);
-    const float l_lse_tot = l_lse + __shfl_xor(l_lse, 32, 64);
-    T* orow = static_cast<T*>(p.o) + q_off;
-    T* torow = static_cast<T*>(p.to) + q_off;
-    {
-        const bool empty = !(l_tot > 0.f);
-        const float inv = empty ? 0.f : 1.f / l_tot;
-        const float rl = r_tot * inv;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-            for (int ig = 0; ig < 4; ++ig) {
-                const int d = 32 * db + 8 * ig + 4 * h;
-                if (row_ok && d < p.D) {
-                    typename V<T>::x4 ov, tv;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float o = u[db][4 * ig + e] * inv;
-                        ov[e] = (T)o;
-                        if constexpr (JVP) tv[e] = (T)(g[db][4 * ig + e] * inv - rl * o);
-                    }
-                    if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
-                    if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
-                }
-            }
-        if (MODE != FA_JVP && h == 0 && row_ok) {
-            p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] =
-                empty ? __builtin_inff() : (m_run + log2f(l_lse_tot)) * kLn2;
-        }
-    }
 }
 
 template <typename T, int MODE>
@@ -396,7 +587,7 @@ int launch_mode(const FaParams& p, int dp, hipStream_t stream) {
         set_error("fa: grid too large");
         return KF_E_UNSUPPORTED;
     }
-    const dim3 grid((unsigned)blocks), block(256);
+    const dim3 grid((unsigned)blocks), block(kThreads);
     switch (dp) {
         case 32: hipLaunchKernelGGL((fa_kernel<T, 32, MODE>), grid, block, 0, stream, p); break;
         case 64: hipLaunchKernelGGL((fa_kernel<T, 64, MODE>), grid, block, 0, stream, p); break;

@@ -63,6 +63,7 @@ template <typename T> struct V {
     typedef T x8 __attribute__((ext_vector_type(8)));
     typedef T x4 __attribute__((ext_vector_type(4)));
 };
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 

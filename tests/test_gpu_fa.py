@@ -292,3 +292,34 @@ def test_baseline_config_fused():
     _, _, tangent2 = flash_attention_fwd_jvp(q, k, v, 2 * tq, 2 * tk, 2 * tv)
     assert torch.equal(tangent2, 2 * tangent)
     assert torch.isfinite(tangent).all() and torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("jump", (30.0, 140.0))
+def test_scores_growing_past_first_tile(dtype, jump):
+    """Keys after the first tile score `jump` log2 units above it.
+
+    The forward kernels fix each row's exponent reference at the max of its
+    first key tile; E = exp2(S - m) then grows to 2^jump.  bf16 holds 2^30 and
+    2^140 overflows; fp16 overflows already at 2^16.  An overflow must send
+    the workgroup to the rescaling scan and still give the oracle's result.
+    """
+    b, n, h, d = 1, 300, 2, 64
+    g = torch.Generator().manual_seed(11)
+    q = torch.full((b, n, h, d), 2.0)
+    k = 0.05 * torch.randn(b, n, h, d, generator=g)
+    # q.k over the later keys: 2 * c * d; scaled by d^-0.5 and log2(e) -> jump.
+    c = jump / (2.0 * d * d ** -0.5 * 1.4426950408889634)
+    k[:, 64:] += c
+    v, tq, tk, tv = (torch.randn(b, n, h, d, generator=g) for _ in range(4))
+    inputs = tuple(x.to(dtype).to(DEV) for x in (q, k, v, tq, tk, tv))
+    ref_out, ref_tangent = orc.attention_jvp(*double_reference(inputs))
+    ref_lse = orc.attention_lse(*double_reference(inputs[:2]))
+    out, lse, tangent = flash_attention_fwd_jvp(*inputs)
+    out2, lse2 = flash_attention(*inputs[:3], return_lse=True)
+    tangent2 = flash_attention_jvp(*inputs, out2, lse2)
+    for o, t, l in ((out, tangent, lse), (out2, tangent2, lse2)):
+        assert torch.isfinite(o).all() and torch.isfinite(t).all() and torch.isfinite(l).all()
+        torch.testing.assert_close(o.cpu().double(), ref_out, **tolerance(dtype))
+        torch.testing.assert_close(t.cpu().double(), ref_tangent, **tolerance(dtype))
+        torch.testing.assert_close(l.cpu().double(), ref_lse, atol=1e-3, rtol=1e-4)
