@@ -232,8 +232,20 @@ void fa_kernel(const FaParams p) {
     constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
     constexpr int DB = DP / 16;        // 16-wide d blocks of the outputs
     typedef typename V<T>::x8 x8;
-    __shared__ __attribute__((aligned(16))) T kside[2][NT][kBK * DP];
-    __shared__ __attribute__((aligned(16))) T vside[2][NT][kBK * DP];
+    // Double-buffered K-side (K, tK) and V-side (V, tV) tiles.  Each buffer is
+    // its own LDS variable so that the compiler's alias analysis separates the
+    // copies into one buffer from the reads of the other.
+    __shared__ __attribute__((aligned(16))) T kside0[NT][kBK * DP];
+    __shared__ __attribute__((aligned(16))) T kside1[NT][kBK * DP];
+    __shared__ __attribute__((aligned(16))) T vside0[NT][kBK * DP];
+    __shared__ __attribute__((aligned(16))) T vside1[NT][kBK * DP];
+    auto lds_tile = [&](auto bufc, auto vsc, int i) -> T* {
+        constexpr int buf = decltype(bufc)::value;
+        if constexpr (decltype(vsc)::value)
+            return buf == 0 ? vside0[i] : vside1[i];
+        else
+            return buf == 0 ? kside0[i] : kside1[i];
+    };
     __shared__ int bail_vote[kWaves];
 
     const int lane = threadIdx.x & 63;
@@ -312,19 +324,20 @@ void fa_kernel(const FaParams p) {
     auto tile_masked = [&](int k0) {
         return (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
     };
-    auto apply_mask = [&](f32x4 (&s)[4], int k0) {
+    // A tile's 64 keys are consumed in two halves of 32 (key blocks 2h, 2h+1).
+    auto apply_mask = [&](f32x4 (&s)[2], int k0, int h) {
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (k0 + 16 * kb + 4 * grp + i > klim) s[kb][i] = -__builtin_inff();
+                if (k0 + 16 * (2 * h + i2) + 4 * grp + i > klim) s[i2][i] = -__builtin_inff();
     };
-    auto row_max = [&](const f32x4 (&s)[4]) {
+    auto row_max = [&](const f32x4 (&s)[2]) {
         float mx = s[0][0];
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
+        for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][i]);
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[i2][i]);
         return row_max4(mx) * c;
     };
 
@@ -369,11 +382,17 @@ void fa_kernel(const FaParams p) {
         // tK) or the V side (V, tV).  The two halves are issued at different
         // points of the previous tile's work so that the wavefronts of a
         // workgroup do not all queue their copies at the same moment.
-        auto issue_side = [&](int tile, bool vs) {
-            const int buf = tile & 1, k0 = tile * kBK;
+        // `bufc` and `vsc` are compile-time constants (std::integral_constant):
+        // with the destination buffer known statically, the compiler can tell
+        // these LDS writes apart from reads of the other buffer and does not
+        // make those reads wait for the copies in flight.
+        auto issue_side = [&](int tile, auto bufc, auto vsc) {
+            constexpr int buf = decltype(bufc)::value;
+            constexpr bool vs = decltype(vsc)::value;
+            const int k0 = tile * kBK;
             const int64_t off = (int64_t)k0 * kv_row_stride;
-            T* const d0 = vs ? vside[buf][0] : kside[buf][0];
-            T* const d1 = vs ? vside[buf][NT - 1] : kside[buf][NT - 1];
+            T* const d0 = lds_tile(bufc, vsc, 0);
+            T* const d1 = lds_tile(bufc, vsc, NT - 1);
             const T* const s0 = (vs ? vbase : kbase) + off;
             const T* const s1 = (vs ? tvbase : tkbase) + off;
             const bool tan = JVP && (vs ? use_tv : use_tk);
@@ -386,30 +405,30 @@ void fa_kernel(const FaParams p) {
                 if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
             }
         };
-        auto issue = [&](int tile) {
-            issue_side(tile, false);
-            issue_side(tile, true);
+        auto issue = [&](int tile, auto bufc) {
+            issue_side(tile, bufc, std::false_type{});
+            issue_side(tile, bufc, std::true_type{});
         };
 
-        // S^T (and tS^T) of the 64 keys of the tile in buffer buf.
-        auto scores = [&](int buf, f32x4 (&s)[4], f32x4 (&ts)[4]) {
-            const T* Kt = kside[buf][0];
-            const T* tKt = kside[buf][NT - 1];
+        // S^T (and tS^T) of key blocks 2h, 2h+1 of the tile in buffer bufc.
+        auto scores = [&](auto bufc, int h, f32x4 (&s)[2], f32x4 (&ts)[2]) {
+            const T* Kt = lds_tile(bufc, std::false_type{}, 0);
+            const T* tKt = lds_tile(bufc, std::false_type{}, NT - 1);
             const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                s[kb] = zero;
-                ts[kb] = zero;
-                const int krow = 16 * kb + (lane & 15);
+            for (int i2 = 0; i2 < 2; ++i2) {
+                s[i2] = zero;
+                ts[i2] = zero;
+                const int krow = 16 * (2 * h + i2) + (lane & 15);
 #pragma unroll
                 for (int ds = 0; ds < DS; ++ds) {
                     const x8 ka = row_chunk<T, DP>(Kt, krow, 4 * ds + grp);
-                    s[kb] = mfma16x16x32(ka, qreg[ds], s[kb]);
+                    s[i2] = mfma16x16x32(ka, qreg[ds], s[i2]);
                     if constexpr (JVP) {
-                        if (use_tq) ts[kb] = mfma16x16x32(ka, tqreg[ds], ts[kb]);
+                        if (use_tq) ts[i2] = mfma16x16x32(ka, tqreg[ds], ts[i2]);
                         if (use_tk) {
                             const x8 tka = row_chunk<T, DP>(tKt, krow, 4 * ds + grp);
-                            ts[kb] = mfma16x16x32(tka, qreg[ds], ts[kb]);
+                            ts[i2] = mfma16x16x32(tka, qreg[ds], ts[i2]);
                         }
                     }
                 }
@@ -418,49 +437,46 @@ void fa_kernel(const FaParams p) {
 
         // E = exp2(S*c + nref) (or P for the JVP mode) and H = E * scale * tS,
         // packed to 16 bits; their rounded values are summed into l and r.
-        auto probs = [&](const f32x4 (&s)[4], const f32x4 (&ts)[4], float nref, u32x2 (&ew)[4],
-                         u32x2 (&hw)[4], Stats& st) {
+        auto probs = [&](const f32x4 (&s)[2], const f32x4 (&ts)[2], float nref, u32x2 (&ew)[2],
+                         u32x2 (&hw)[2], Stats& st) {
             float esum = 0.f;
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+            for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const float e0 = fast_exp2(fmaf(s[kb][2 * j], c, nref));
-                    const float e1 = fast_exp2(fmaf(s[kb][2 * j + 1], c, nref));
+                    const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref));
+                    const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref));
                     if constexpr (MODE != FA_JVP) esum += e0 + e1;
                     const unsigned pe = Pk<T>::cvt(e0, e1);
-                    ew[kb][j] = pe;
+                    ew[i2][j] = pe;
                     st.l_run = Pk<T>::sum_into(pe, st.l_run);
                     if constexpr (JVP) {
-                        const unsigned ph = Pk<T>::cvt(e0 * (ts[kb][2 * j] * p.scale),
-                                                       e1 * (ts[kb][2 * j + 1] * p.scale));
-                        hw[kb][j] = ph;
+                        const unsigned ph = Pk<T>::cvt(e0 * (ts[i2][2 * j] * p.scale),
+                                                       e1 * (ts[i2][2 * j + 1] * p.scale));
+                        hw[i2][j] = ph;
                         st.r_run = Pk<T>::sum_into(ph, st.r_run);
                     }
                 }
             if constexpr (MODE != FA_JVP) st.l_lse += esum;
         };
 
-        // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the tile in buffer buf.
-        auto pv = [&](f32x4 (&u)[DB], f32x4 (&g)[DB], int buf, const u32x2 (&ew)[4], const u32x2 (&hw)[4]) {
-            const T* Vt = vside[buf][0];
-            const T* tVt = vside[buf][NT - 1];
+        // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the 32 keys of half h
+        // of the tile in buffer bufc.
+        auto pv = [&](f32x4 (&u)[DB], f32x4 (&g)[DB], auto bufc, int h, const u32x2 (&ew)[2],
+                      const u32x2 (&hw)[2]) {
+            const T* Vt = lds_tile(bufc, std::true_type{}, 0);
+            const T* tVt = lds_tile(bufc, std::true_type{}, NT - 1);
+            const x8 eb = __builtin_bit_cast(x8, u32x4{ew[0][0], ew[0][1], ew[1][0], ew[1][1]});
+            const x8 hb = __builtin_bit_cast(x8, u32x4{hw[0][0], hw[0][1], hw[1][0], hw[1][1]});
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const x8 eb = __builtin_bit_cast(x8, u32x4{ew[2 * kk][0], ew[2 * kk][1], ew[2 * kk + 1][0],
-                                                           ew[2 * kk + 1][1]});
-                const x8 hb = __builtin_bit_cast(x8, u32x4{hw[2 * kk][0], hw[2 * kk][1], hw[2 * kk + 1][0],
-                                                           hw[2 * kk + 1][1]});
-#pragma unroll
-                for (int db = 0; db < DB; ++db) {
-                    const x8 va = vt_operand<T, DP>(Vt, kk, db, lane);
-                    u[db] = mfma16x16x32(va, eb, u[db]);
-                    if constexpr (JVP) {
-                        g[db] = mfma16x16x32(va, hb, g[db]);
-                        if (use_tv) {
-                            const x8 tva = vt_operand<T, DP>(tVt, kk, db, lane);
-                            g[db] = mfma16x16x32(tva, eb, g[db]);
-                        }
+            for (int db = 0; db < DB; ++db) {
+                const x8 va = vt_operand<T, DP>(Vt, h, db, lane);
+                u[db] = mfma16x16x32(va, eb, u[db]);
+                if constexpr (JVP) {
+                    g[db] = mfma16x16x32(va, hb, g[db]);
+                    if (use_tv) {
+                        const x8 tva = vt_operand<T, DP>(tVt, h, db, lane);
+                        g[db] = mfma16x16x32(tva, eb, g[db]);
                     }
                 }
             }
@@ -478,29 +494,38 @@ void fa_kernel(const FaParams p) {
             zero_acc(g);
             Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
             float nref = nref_lse;
-            f32x4 s[4], ts[4];
-            u32x2 ew[4], hw[4];
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) hw[kb] = u32x2{0u, 0u};
-            if (ntiles > 0) issue(0);
-            for (int t = 0; t < ntiles; ++t) {
-                const int buf = t & 1, k0 = t * kBK;
+            f32x4 s[2], ts[2];
+            u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
+            // One key tile; tile t lives in buffer t & 1 == decltype(bufc)::value.
+            auto step = [&](int t, auto bufc) {
+                constexpr int buf = decltype(bufc)::value;
+                const std::integral_constant<int, buf ^ 1> nbuf;
+                const int k0 = t * kBK;
+                const bool masked = tile_masked(k0);
                 wait_vmem();
                 __syncthreads();  // tile t resident; every wavefront is done with tile t-1
-                if (t + 1 < ntiles) issue_side(t + 1, false);
-                scores(buf, s, ts);
-                if (t + 1 < ntiles) issue_side(t + 1, true);
-                if (tile_masked(k0)) apply_mask(s, k0);
-                if constexpr (MODE != FA_JVP) {
-                    if (t == 0) {
-                        // Every non-empty row has a valid key in its first tile
-                        // (masks only cut keys off at the end).
-                        st.m_run = row_max(s);
-                        nref = st.m_run == -__builtin_inff() ? 0.f : -st.m_run;
+                if (t + 1 < ntiles) issue_side(t + 1, nbuf, std::false_type{});
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    scores(bufc, h, s, ts);
+                    if (h == 0 && t + 1 < ntiles) issue_side(t + 1, nbuf, std::true_type{});
+                    if (masked) apply_mask(s, k0, h);
+                    if constexpr (MODE != FA_JVP) {
+                        if (t == 0 && h == 0) {
+                            // Every non-empty row has a valid key among the
+                            // first 32 (masks only cut keys off at the end).
+                            st.m_run = row_max(s);
+                            nref = st.m_run == -__builtin_inff() ? 0.f : -st.m_run;
+                        }
                     }
+                    probs(s, ts, nref, ew, hw, st);
+                    pv(u, g, bufc, h, ew, hw);
                 }
-                probs(s, ts, nref, ew, hw, st);
-                pv(u, g, buf, ew, hw);
+            };
+            if (ntiles > 0) issue(0, std::integral_constant<int, 0>{});
+            for (int t = 0; t < ntiles; t += 2) {
+                step(t, std::integral_constant<int, 0>{});
+                if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
             }
             if constexpr (MODE == FA_JVP) {
                 epilogue(u, g, st);
@@ -537,38 +562,43 @@ void fa_kernel(const FaParams p) {
             zero_acc(u);
             zero_acc(g);
             Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
+            // Copy, wait and consume one tile at a time, always in buffer 0.
+            const std::integral_constant<int, 0> buf0;
             for (int t = 0; t < ntiles; ++t) {
-                const int buf = t & 1, k0 = t * kBK;
-                issue(t);
+                const int k0 = t * kBK;
+                issue(t, buf0);
                 wait_vmem();
                 __syncthreads();
-                f32x4 s[4], ts[4];
-                u32x2 ew[4], hw[4] = {u32x2{0u, 0u}, u32x2{0u, 0u}, u32x2{0u, 0u}, u32x2{0u, 0u}};
-                scores(buf, s, ts);
-                if (tile_masked(k0)) apply_mask(s, k0);
-                // Raise the reference only when the max grew by more than 2^8:
-                // E stays <= 256.  A row leaving m = -inf gets alpha =
-                // exp2(-inf) = 0 on its all-zero state.
-                const float mx = row_max(s);
-                const bool upd = mx > st.m_run + kRescaleThreshold;
-                const float alpha = upd ? fast_exp2(st.m_run - mx) : 1.f;
-                if (upd) {
-                    st.m_run = mx;
-                    st.l_run *= alpha;
-                    st.r_run *= alpha;
-                    st.l_lse *= alpha;
-                }
-                if (__any(upd)) {
 #pragma unroll
-                    for (int db = 0; db < DB; ++db)
+                for (int h = 0; h < 2; ++h) {
+                    f32x4 s[2], ts[2];
+                    u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
+                    scores(buf0, h, s, ts);
+                    if (tile_masked(k0)) apply_mask(s, k0, h);
+                    // Raise the reference only when the max grew by more than
+                    // 2^8: E stays <= 256.  A row leaving m = -inf gets alpha =
+                    // exp2(-inf) = 0 on its all-zero state.
+                    const float mx = row_max(s);
+                    const bool upd = mx > st.m_run + kRescaleThreshold;
+                    const float alpha = upd ? fast_exp2(st.m_run - mx) : 1.f;
+                    if (upd) {
+                        st.m_run = mx;
+                        st.l_run *= alpha;
+                        st.r_run *= alpha;
+                        st.l_lse *= alpha;
+                    }
+                    if (__any(upd)) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            u[db][i] *= alpha;
-                            g[db][i] *= alpha;
-                        }
+                        for (int db = 0; db < DB; ++db)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                u[db][i] *= alpha;
+                                g[db][i] *= alpha;
+                            }
+                    }
+                    probs(s, ts, st.m_run == -__builtin_inff() ? 0.f : -st.m_run, ew, hw, st);
+                    pv(u, g, buf0, h, ew, hw);
                 }
-                probs(s, ts, st.m_run == -__builtin_inff() ? 0.f : -st.m_run, ew, hw, st);
-                pv(u, g, buf, ew, hw);
                 __syncthreads();
             }
             epilogue(u, g, st);

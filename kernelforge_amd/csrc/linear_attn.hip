@@ -14,8 +14,8 @@
 //      V per token) through LDS and accumulates S with v_mfma_f32_32x32x16; the
 //      token-major operands are read with ds_read_b64_tr_b16.  z accumulates on
 //      the VALU from the same registers.  Partials [B][H][splits][D+1][D] fp32.
-//   2. linattn_reduce_kernel  grid (H, B): sums the partials in split order
-//      (fixed order: deterministic, no atomics).
+//   2. linattn_reduce_kernel  one thread per state element: sums the partials in
+//      split order (fixed order: deterministic, no atomics).
 //   3. linattn_out_kernel     grid (ceil(N/128), ceil(H/4), B): one wavefront per
 //      head keeps S and z in registers as hi+lo 16-bit pairs (so the products
 //      carry ~16 mantissa bits of the fp32 state) and streams relu(q) straight
@@ -33,52 +33,74 @@ constexpr int kD = 32;              // head dim of the MFMA path
 constexpr int kState = (kD + 1) * kD;
 constexpr int kTT = 64;             // tokens per state tile
 constexpr int kRS = 72;             // LDS row stride (elements) of a 64-channel row
-constexpr int kOutTokens = 128;     // tokens per output workgroup
+constexpr int kOutTokens = 64;      // tokens per output workgroup
 
 // --------------------------------------------------------------------------
 // 1. Split-state producer (MFMA).
 // --------------------------------------------------------------------------
+// Workgroup barrier that leaves global loads in flight.  __syncthreads()
+// also waits for every outstanding global load (vmcnt(0)), which would drain
+// the register prefetch below at each tile; here only this wave's LDS
+// traffic is completed (lgkmcnt(0)) before s_barrier.  The empty asm
+// statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_keep_loads() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Global -> register staging of one 64-token tile of a head pair: 4 x 16 B per
+// thread.  Chunk c = i*256 + tid: token c/16, part (c/8)%2 (0 = K, 1 = V),
+// 16-byte segment c%8 of the 128-byte two-head span, so every load
+// instruction of a wave covers 4 tokens x 2 whole 128-byte lines.  Addresses
+// are clamped into the split (token t_end-1) and onto the present head, so
+// the number of loads never depends on the data; the clamped duplicates are
+// zeroed when the tile is stored to LDS.
+template <typename T>
+__device__ __forceinline__ void state_gload(u32x4 (&reg)[4], const T* __restrict__ qkv, int64_t b,
+                                            int N, int64_t C, int h0, int nh, int t0, int t_end,
+                                            int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = i * 256 + tid;
+        const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
+        const int t = min(t0 + tok, t_end - 1);
+        const int sg = seg < nh * 4 ? seg : seg - 4;
+        const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (1 + part) * C + (int64_t)h0 * kD + sg * 8;
+        reg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict__ qkv,
                                                             float* __restrict__ partial, int N,
                                                             int H, int split_len, int splits) {
-    const int s = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    // Head pairs vary fastest over the grid, so the workgroups resident at one
+    // time read neighbouring 128-byte spans of the same token rows.
+    const int g = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t C = (int64_t)H * kD;
     const int h0 = 2 * g;
     const int nh = min(2, H - h0);
-    const int t_begin = s * split_len;
+    const int t_begin = s * split_len;            // < N: the host sizes the grid
     const int t_end = min(N, t_begin + split_len);
 
-    __shared__ __attribute__((aligned(16))) T tile[2][2][kTT * kRS];  // [buf][K,V][tok*kRS+ch]
-    __shared__ float comb[2][64][17];
+    // [buf][K,V][tok*kRS+ch]; after the scan the same memory combines the
+    // two token halves ([head slot][lane][16 accumulators + z]).
+    __shared__ __attribute__((aligned(16))) T tile[2][2][kTT * kRS];
+    static_assert(sizeof(tile) >= 2 * 64 * 17 * sizeof(float), "combine buffer fits in the tiles");
+    float (*comb)[64][17] = reinterpret_cast<float (*)[64][17]>(&tile[0][0][0]);
 
-    // Global -> register staging: 4 x 16 B per thread per tile.  Chunk c:
-    // token c/16, part (c/8)%2 (0 = K, 1 = V), 16-byte segment c%8 of the
-    // 128-byte two-head span.
-    u32x4 reg[4];
-    auto gload = [&](int t0) {
+    // Tile rows at or past t_end are stored as zeros; ReLU is applied to K.
+    auto lstore = [&](const u32x4 (&reg)[4], int buf, int t0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = i * 256 + tid;
             const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
-            const int t = t0 + tok;
-            if (t < t_end && seg < nh * 4) {
-                const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (1 + part) * C +
-                               (int64_t)h0 * kD + seg * 8;
-                u32x4 v = *reinterpret_cast<const u32x4*>(src);
-                reg[i] = part == 0 ? relu_packed16(v) : v;
-            } else {
-                reg[i] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = i * 256 + tid;
-            const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
-            *reinterpret_cast<u32x4*>(&tile[buf][part][tok * kRS + seg * 8]) = reg[i];
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            const u32x4 v = t0 + tok < t_end ? (part == 0 ? relu_packed16(reg[i]) : reg[i]) : z;
+            *reinterpret_cast<u32x4*>(&tile[buf][part][tok * kRS + seg * 8]) = v;
         }
     };
 
@@ -90,15 +112,7 @@ __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict_
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     float zsum = 0.f;
 
-    const int ntile = t_end > t_begin ? (t_end - t_begin + kTT - 1) / kTT : 0;
-    if (ntile > 0) {
-        gload(t_begin);
-        lstore(0);
-    }
-    __syncthreads();
-    for (int it = 0; it < ntile; ++it) {
-        const int buf = it & 1;
-        if (it + 1 < ntile) gload(t_begin + (it + 1) * kTT);
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int row = 32 * th + 16 * ks + 8 * (G >> 1) + (j16 >> 2);
@@ -119,11 +133,37 @@ __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict_
 #pragma unroll
             for (int j = 0; j < 8; ++j) zsum += (float)bk[j];
         }
-        if (it + 1 < ntile) lstore(buf ^ 1);
-        __syncthreads();
+    };
+
+    // Three tiles stay in flight in registers while one is consumed from LDS.
+    // Tile j is loaded into register set j % 3 and stored to LDS buffer j % 2
+    // one iteration ahead of its use.  The register set is chosen at compile
+    // time (the loop is unrolled by three), and every step issues its loads
+    // (past the end of the split they re-read row t_end-1), so the compiler's
+    // wait before each LDS store is an exact count of younger loads.
+    const int ntile = (t_end - t_begin + kTT - 1) / kTT;  // >= 1
+    u32x4 r0[4], r1[4], r2[4];
+    state_gload<T>(r0, qkv, b, N, C, h0, nh, t_begin, t_end, tid);
+    state_gload<T>(r1, qkv, b, N, C, h0, nh, t_begin + kTT, t_end, tid);
+    state_gload<T>(r2, qkv, b, N, C, h0, nh, t_begin + 2 * kTT, t_end, tid);
+    lstore(r0, 0, t_begin);
+    barrier_keep_loads();
+    // Step it: LDS buffer it&1 holds tile it; `nx` holds tile it+1; `fr` is
+    // free and receives tile it+3.
+    auto step = [&](int it, u32x4 (&fr)[4], u32x4 (&nx)[4]) {
+        state_gload<T>(fr, qkv, b, N, C, h0, nh, t_begin + (it + 3) * kTT, t_end, tid);
+        compute(it & 1);
+        lstore(nx, (it + 1) & 1, t_begin + (it + 1) * kTT);
+        barrier_keep_loads();
+    };
+    for (int it = 0; it < ntile; it += 3) {
+        step(it, r0, r1);
+        if (it + 1 < ntile) step(it + 1, r1, r2);
+        if (it + 2 < ntile) step(it + 2, r2, r0);
     }
 
     // Combine the two token halves of each head, then write the partial.
+    __syncthreads();
     if (th == 1) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) comb[hw][lane][i] = acc[i];
@@ -151,50 +191,91 @@ __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict_
 // --------------------------------------------------------------------------
 // 2. Fixed-order reduction of the split partials.
 // --------------------------------------------------------------------------
+// One thread per state element of one (batch, head); the partials of all
+// splits are loaded eight at a time before they are added, in split order
+// (deterministic, no atomics).
 __global__ __launch_bounds__(256) void linattn_reduce_kernel(const float* __restrict__ partial,
-                                                             float* __restrict__ state, int H,
-                                                             int splits, int state_size) {
-    const int h = blockIdx.x, b = blockIdx.y;
-    const float* P = partial + (int64_t)(b * H + h) * splits * state_size;
-    float* S = state + (int64_t)(b * H + h) * state_size;
-    for (int e = threadIdx.x; e < state_size; e += 256) {
-        float acc = 0.f;
-        for (int s = 0; s < splits; ++s) acc += P[(int64_t)s * state_size + e];
-        S[e] = acc;
+                                                             float* __restrict__ state,
+                                                             int64_t n_heads, int splits,
+                                                             int state_size) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= n_heads * state_size) return;
+    const int64_t bh = idx / state_size;
+    const int e = (int)(idx - bh * state_size);
+    const float* P = partial + bh * splits * (int64_t)state_size + e;
+    float acc = 0.f;
+    int s = 0;
+    for (; s + 8 <= splits; s += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = P[(int64_t)(s + j) * state_size];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += v[j];
     }
+    for (; s < splits; ++s) acc += P[(int64_t)s * state_size];
+    state[idx] = acc;
 }
 
 // --------------------------------------------------------------------------
 // 3. Output contraction (MFMA, state in registers).
 // --------------------------------------------------------------------------
-template <typename TO> struct Store4;
-template <> struct Store4<float> {
-    __device__ static void run(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+// Stores of the numerator pair (n0: channels 4kg..4kg+3, n1: 16+4kg..) after
+// v_permlane16_swap has exchanged n1 of the even 16-lane groups with n0 of
+// the odd ones: an even group then holds channels 4kg..4kg+7, an odd group
+// 16+4(kg-1)..16+4(kg-1)+7, so each lane writes 8 consecutive channels.
+template <typename TO> struct Store8;
+template <> struct Store8<float> {
+    __device__ static void run(float* p, f32x4 a, f32x4 b) {
+        *reinterpret_cast<f32x4*>(p) = a;
+        *reinterpret_cast<f32x4*>(p + 4) = b;
+    }
 };
-template <typename TO> struct Store4 {
-    __device__ static void run(TO* p, f32x4 v) {
-        typename V<TO>::x4 o;
+template <typename TO> struct Store8 {
+    __device__ static void run(TO* p, f32x4 a, f32x4 b) {
+        typename V<TO>::x8 o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (TO)v[i];
-        *reinterpret_cast<typename V<TO>::x4*>(p) = o;
+        for (int i = 0; i < 4; ++i) {
+            o[i] = (TO)a[i];
+            o[i + 4] = (TO)b[i];
+        }
+        *reinterpret_cast<typename V<TO>::x8*>(p) = o;
     }
 };
 
+// Output workgroup: 4 wavefronts = 4 consecutive heads (one 256-byte span
+// of each token row) x kOutTokens tokens.  q arrives with whole-line loads
+// (each wave instruction: 4 tokens x 256 B) and is staged in LDS; each wave
+// then reads the MFMA B operand of its own head (16 tokens x 32 channels)
+// from LDS.  The normalised rows go back through LDS so that the stores are
+// whole lines too.  Loads and stores that split 128-byte lines between
+// wavefronts ran at ~60% of the whole-line rate on MI355X.
 template <typename T, typename TO>
 __global__ __launch_bounds__(256) void linattn_out_kernel(const T* __restrict__ qkv,
                                                           const float* __restrict__ state,
                                                           TO* __restrict__ out, int N, int H,
                                                           float eps) {
+    constexpr int TT = kOutTokens;
+    constexpr int QR = 4 * kD + 8;            // q tile row stride (elements), padded
+    constexpr int OB = 4 * kD * sizeof(TO);   // output bytes per token row of 4 heads
+    constexpr int OR = OB + 16;               // out tile row stride (bytes), padded
+    __shared__ __attribute__((aligned(16))) T qt[TT * QR];
+    __shared__ __attribute__((aligned(16))) unsigned char ot[TT * OR];
+
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int b = blockIdx.z;
-    const int h = blockIdx.y * 4 + wave;
-    if (h >= H) return;
+    const int hq0 = blockIdx.x * 4;           // head quads vary fastest over the grid
+    const int nhq = min(4, H - hq0);
+    const int h = hq0 + wave;
+    const int hs = h < H ? h : hq0;           // a missing head computes on head hq0, unstored
     const int64_t C = (int64_t)H * kD;
-    const float* S = state + (int64_t)(b * H + h) * kState;
     const int m16 = lane & 15, kg = lane >> 4;
+    const int lr = lane >> 4, lc = lane & 15;  // whole-line load: token row lr, 16-byte chunk lc
+    const int lcc = lc < nhq * 4 ? lc : 0;
 
-    // A operands: rows r = 16*mb + m16, k = c = 8*kg + j; the third operand
-    // repeats z on every row.
+    // S and z of this wave's head as hi+lo 16-bit A operands: rows
+    // r = 16*mb + m16, k = c = 8*kg + j; the third operand repeats z on every
+    // row, so the denominator lands in the same lanes as the numerator.
+    const float* S = state + (int64_t)(b * H + hs) * kState;
     float sv[2][8], zv[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -233,42 +314,66 @@ __global__ __launch_bounds__(256) void linattn_out_kernel(const T* __restrict__ 
         zlo[j] = (T)(x - (float)hi);
     }
 
-    const int t_block = blockIdx.x * kOutTokens;
-    const int t_stop = min(N, t_block + kOutTokens);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    for (int t0 = t_block; t0 < t_stop; t0 += 64) {
-        u32x4 qv[4];
+    const int c0 = (kg & 1) ? 16 + 4 * (kg - 1) : 4 * kg;
+    constexpr int LPR = OB / 16;              // lanes per output row (16 bf16/f16, 32 fp32)
+    constexpr int RPI = 64 / LPR;             // output rows per store instruction
+    const int sr = lane / LPR, sc = lane % LPR;
+    const bool sc_ok = sc * 16 < nhq * kD * (int)sizeof(TO);
+
+    const int n_blocks = (N + TT - 1) / TT;
+    for (int tb = blockIdx.y; tb < n_blocks; tb += gridDim.y) {
+        const int t_block = tb * TT;
+        const int t_stop = min(N, t_block + TT);
+        // Rows past t_stop re-read row t_stop-1; their results are not stored.
+        u32x4 qv[TT / 16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int t = t0 + 16 * u + m16;
-            if (t < t_stop) {
-                const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (int64_t)h * kD + 8 * kg;
-                qv[u] = relu_packed16(*reinterpret_cast<const u32x4*>(src));
-            } else {
-                qv[u] = u32x4{0u, 0u, 0u, 0u};
-            }
+        for (int k = 0; k < TT / 16; ++k) {
+            const int t = min(t_block + 4 * (4 * k + wave) + lr, t_stop - 1);
+            const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (int64_t)hq0 * kD + lcc * 8;
+            qv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
         }
+        if (tb != blockIdx.y) __syncthreads();  // the previous block's LDS reads are done
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const typename V<T>::x8 bq = __builtin_bit_cast(typename V<T>::x8, qv[u]);
+        for (int k = 0; k < TT / 16; ++k) {
+            const int row = 4 * (4 * k + wave) + lr;
+            *reinterpret_cast<u32x4*>(&qt[row * QR + lc * 8]) = relu_packed16(qv[k]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TT / 16; ++u) {
+            const int row = 16 * u + m16;
+            const typename V<T>::x8 bq =
+                *reinterpret_cast<const typename V<T>::x8*>(&qt[row * QR + wave * kD + 8 * kg]);
             f32x4 n0 = mfma16x16x32(shi[0], bq, zero);
             n0 = mfma16x16x32(slo[0], bq, n0);
             f32x4 n1 = mfma16x16x32(shi[1], bq, zero);
             n1 = mfma16x16x32(slo[1], bq, n1);
             f32x4 dn = mfma16x16x32(zhi, bq, zero);
             dn = mfma16x16x32(zlo, bq, dn);
-            const int t = t0 + 16 * u + m16;
-            if (t < t_stop) {
-                const float den = dn[0] + eps;
-                f32x4 o0, o1;
+            const float inv = 1.0f / (dn[0] + eps);
+            f32x4 lo, hi;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    o0[i] = n0[i] / den;
-                    o1[i] = n1[i] / den;
-                }
-                TO* dst = out + ((int64_t)b * N + t) * C + (int64_t)h * kD + 4 * kg;
-                Store4<TO>::run(dst, o0);
-                Store4<TO>::run(dst + 16, o1);
+            for (int i = 0; i < 4; ++i) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(n0[i] * inv),
+                                                                __float_as_uint(n1[i] * inv), false, false);
+                lo[i] = __uint_as_float(r[0]);
+                hi[i] = __uint_as_float(r[1]);
+            }
+            // Even groups now hold (n0 own, n0 of the odd partner) = channels
+            // 4kg..4kg+7; odd groups (n1 of the even partner, n1 own) = channels
+            // 16+4(kg-1)..16+4(kg-1)+7.
+            Store8<TO>::run(reinterpret_cast<TO*>(&ot[row * OR + (wave * kD + c0) * sizeof(TO)]), lo, hi);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < TT / (4 * RPI); ++k) {
+            const int row = RPI * (4 * k + wave) + sr;
+            const int t = t_block + row;
+            if (t < t_stop && sc_ok) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(&ot[row * OR + sc * 16]);
+                unsigned char* dst = reinterpret_cast<unsigned char*>(out + ((int64_t)b * N + t) * C + (int64_t)hq0 * kD);
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + sc * 16));
             }
         }
     }
@@ -285,7 +390,7 @@ __global__ __launch_bounds__(256) void linattn_state_generic(const T* __restrict
                                                              int H, int split_len, int splits) {
     constexpr int SS = (DG + 1) * DG;
     constexpr int EPT = (SS + 255) / 256;
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
     const int64_t C = (int64_t)H * DG;
     const int t_begin = s * split_len, t_end = min(N, t_begin + split_len);
     __shared__ float kt[kGT][DG], vt[kGT][DG + 1];
@@ -333,13 +438,15 @@ __global__ __launch_bounds__(256) void linattn_out_generic(const T* __restrict__
                                                            float eps) {
     constexpr int SS = (DG + 1) * DG;
     constexpr int TPI = 256 / DG > 0 ? 256 / DG : 1;  // tokens per pass (one thread per (t, r))
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.x, b = blockIdx.z;
     const int64_t C = (int64_t)H * DG;
     __shared__ float st[SS];
     __shared__ float qt[TPI][DG];
     const float* S = state + (int64_t)(b * H + h) * SS;
     for (int i = threadIdx.x; i < SS; i += 256) st[i] = S[i];
-    const int t_block = blockIdx.x * kOutTokens;
+    const int n_blocks = (N + kOutTokens - 1) / kOutTokens;
+    for (int tb = blockIdx.y; tb < n_blocks; tb += gridDim.y) {
+    const int t_block = tb * kOutTokens;
     const int t_stop = min(N, t_block + kOutTokens);
     for (int t0 = t_block; t0 < t_stop; t0 += TPI) {
         __syncthreads();
@@ -362,11 +469,18 @@ __global__ __launch_bounds__(256) void linattn_out_generic(const T* __restrict__
             }
         }
     }
+    }
 }
 
 // --------------------------------------------------------------------------
 // Host side.
 // --------------------------------------------------------------------------
+// Token-block dimension of the output grids (the kernels loop past 65535).
+unsigned out_grid_y(int N) {
+    const int blocks = (N + kOutTokens - 1) / kOutTokens;
+    return (unsigned)(blocks < 65535 ? blocks : 65535);
+}
+
 int64_t split_len_for(int64_t N, int64_t splits, int64_t align) {
     int64_t len = (N + splits - 1) / splits;
     return (len + align - 1) / align * align;
@@ -375,14 +489,15 @@ int64_t split_len_for(int64_t N, int64_t splits, int64_t align) {
 template <typename T, typename TO>
 int run_mfma(const void* qkv, void* out, float* partial, float* state, int B, int N, int H,
              int splits, int split_len, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL((linattn_state_kernel<T>), dim3(splits, (H + 1) / 2, B), dim3(256), 0,
+    hipLaunchKernelGGL((linattn_state_kernel<T>), dim3((H + 1) / 2, splits, B), dim3(256), 0,
                        stream, static_cast<const T*>(qkv), partial, N, H, split_len, splits);
     if (int rc = check_launch("linattn_state_kernel launch")) return rc;
-    hipLaunchKernelGGL(linattn_reduce_kernel, dim3(H, B), dim3(256), 0, stream, partial, state, H,
-                       splits, kState);
+    const int64_t n_state = (int64_t)B * H * (kState);
+    hipLaunchKernelGGL(linattn_reduce_kernel, dim3((unsigned)((n_state + 255) / 256)), dim3(256), 0,
+                       stream, partial, state, (int64_t)B * H, splits, kState);
     if (int rc = check_launch("linattn_reduce_kernel launch")) return rc;
     hipLaunchKernelGGL((linattn_out_kernel<T, TO>),
-                       dim3((N + kOutTokens - 1) / kOutTokens, (H + 3) / 4, B), dim3(256), 0,
+                       dim3((H + 3) / 4, out_grid_y(N), B), dim3(256), 0,
                        stream, static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);
     return check_launch("linattn_out_kernel launch");
 }
@@ -390,14 +505,15 @@ int run_mfma(const void* qkv, void* out, float* partial, float* state, int B, in
 template <typename T, typename TO, int DG>
 int run_generic(const void* qkv, void* out, float* partial, float* state, int B, int N, int H,
                 int splits, int split_len, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(splits, H, B), dim3(256), 0, stream,
+    hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(H, splits, B), dim3(256), 0, stream,
                        static_cast<const T*>(qkv), partial, N, H, split_len, splits);
     if (int rc = check_launch("linattn_state_generic launch")) return rc;
-    hipLaunchKernelGGL(linattn_reduce_kernel, dim3(H, B), dim3(256), 0, stream, partial, state, H,
-                       splits, (DG + 1) * DG);
+    const int64_t n_state = (int64_t)B * H * ((DG + 1) * DG);
+    hipLaunchKernelGGL(linattn_reduce_kernel, dim3((unsigned)((n_state + 255) / 256)), dim3(256), 0,
+                       stream, partial, state, (int64_t)B * H, splits, (DG + 1) * DG);
     if (int rc = check_launch("linattn_reduce_kernel launch")) return rc;
     hipLaunchKernelGGL((linattn_out_generic<T, TO, DG>),
-                       dim3((N + kOutTokens - 1) / kOutTokens, H, B), dim3(256), 0, stream,
+                       dim3(H, out_grid_y(N), B), dim3(256), 0, stream,
                        static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);
     return check_launch("linattn_out_generic launch");
 }
@@ -489,9 +605,10 @@ extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64
                (long long)workspace_bytes);
     const bool mfma = dim == kD && in_dtype != KF_F32 && (uintptr_t)qkv % 16 == 0 &&
                       (uintptr_t)out % 16 == 0;
-    const int64_t split_len = split_len_for(seq_len, splits, mfma ? kTT : kGT);
+    // The split index is the y grid dimension (at most 65535 blocks).
+    const int64_t split_len = split_len_for(seq_len, splits < 65535 ? splits : 65535, mfma ? kTT : kGT);
     const int64_t eff_splits = (seq_len + split_len - 1) / split_len;
-    KF_REQUIRE(eff_splits <= 0x7fffffff, KF_E_UNSUPPORTED, "linattn: too many splits");
+    KF_REQUIRE(eff_splits <= 65535, KF_E_UNSUPPORTED, "linattn: too many splits");
     const int64_t state_size = (dim + 1) * dim;
     float* partial = static_cast<float*>(workspace);
     float* state = partial + batch * heads * state_size * splits;

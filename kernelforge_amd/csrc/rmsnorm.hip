@@ -10,21 +10,24 @@
 // Layout: the row is split into 16-byte vectors; vector j of a row lives in
 // lane (j % 64) of wave-slice (j / 64) % WPR at register slot j / (64*WPR),
 // so every load/store instruction of a wave covers a contiguous 1 KiB span.
-// A row is owned by WPR waves (WPR = 1 needs no LDS and no barrier).
+// A row is owned by WPR waves (WPR = 1 needs no LDS and no barrier).  Rows of
+// 4-16 KiB are spread over 2-8 waves with 2 vectors per lane: short-lived
+// waves with few loads each kept the HBM queues fuller than long-lived ones
+// in sweeps of (VPT, WPR, block size) on MI355X.
 #include "kf_common.h"
 
 namespace kf {
 namespace {
 
-constexpr int kBlock = 256;  // 4 waves
+constexpr int kBlock = 256;  // 4 waves (generic kernel)
 
-template <typename T, int VPT, int WPR, bool HAS_W>
-__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const T* __restrict__ x,
-                                                             const T* __restrict__ w,
-                                                             T* __restrict__ y, int64_t rows,
-                                                             int dim, float eps) {
+template <typename T, int VPT, int WPR, int WAVES, bool HAS_W>
+__global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* __restrict__ x,
+                                                                 const T* __restrict__ w,
+                                                                 T* __restrict__ y, int64_t rows,
+                                                                 int dim, float eps) {
     constexpr int VEC = 16 / sizeof(T);
-    constexpr int ROWS_PER_BLOCK = 4 / WPR;
+    constexpr int ROWS_PER_BLOCK = WAVES / WPR;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int row_in_block = wave / WPR;
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(const T* __restrict
     }
     ss = wave_sum(ss);
     if constexpr (WPR > 1) {
-        __shared__ float part[4];
+        __shared__ float part[WAVES];
         if (lane == 0) part[wave] = ss;
         __syncthreads();
         float t = 0.f;
@@ -119,15 +122,16 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const T* __rest
     }
 }
 
-template <typename T, int VPT, int WPR, bool HAS_W>
+template <typename T, int VPT, int WPR, int WAVES, bool HAS_W>
 int launch_vec(const void* x, const void* w, void* y, int64_t rows, int64_t dim, float eps,
                hipStream_t stream) {
-    constexpr int ROWS_PER_BLOCK = 4 / WPR;
+    static_assert(WAVES % WPR == 0, "a block holds whole rows");
+    constexpr int ROWS_PER_BLOCK = WAVES / WPR;
     const int64_t blocks = (rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK;
     KF_REQUIRE(blocks <= 0x7fffffff, KF_E_UNSUPPORTED, "rmsnorm: %lld rows exceed the grid limit",
                (long long)rows);
-    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, VPT, WPR, HAS_W>), dim3((unsigned)blocks),
-                       dim3(kBlock), 0, stream, static_cast<const T*>(x),
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, VPT, WPR, WAVES, HAS_W>), dim3((unsigned)blocks),
+                       dim3(64 * WAVES), 0, stream, static_cast<const T*>(x),
                        static_cast<const T*>(w), static_cast<T*>(y), rows, (int)dim, eps);
     return check_launch("rmsnorm_vec_kernel launch");
 }
@@ -141,13 +145,14 @@ int dispatch(const void* x, const void* w, void* y, int64_t rows, int64_t dim, f
                          (!HAS_W || (uintptr_t)w % 16 == 0) && (dim % VEC == 0);
     const int64_t nvec = dim / VEC;
     if (aligned) {
-        // Smallest power-of-two vector count per lane, fewest waves per row.
-        if (nvec <= 64) return launch_vec<T, 1, 1, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 128) return launch_vec<T, 2, 1, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 256) return launch_vec<T, 4, 1, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 512) return launch_vec<T, 8, 1, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 1024) return launch_vec<T, 8, 2, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 2048) return launch_vec<T, 8, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
+        // (vectors per lane, waves per row, waves per block).
+        if (nvec <= 64) return launch_vec<T, 1, 1, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 128) return launch_vec<T, 2, 1, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 256) return launch_vec<T, 2, 2, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 512) return launch_vec<T, 2, 4, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 1024) return launch_vec<T, 2, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 2048) return launch_vec<T, 4, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 4096) return launch_vec<T, 8, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
     }
     KF_REQUIRE(rows <= 0x7fffffff, KF_E_UNSUPPORTED, "rmsnorm: %lld rows exceed the grid limit",
                (long long)rows);
