@@ -223,7 +223,9 @@ def cpu_baselines(rows=16384, hidden=4096) -> dict:
 
 
 def load_traffic() -> dict:
-    """Per-kernel HBM bytes per dispatch measured with rocprofv3 --pmc (committed under profiles/)."""
+    """HBM bytes per launch, "kernel:workload" -> bytes, from rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE scaled by the same counters on a 256 MiB copy (profiles/traffic.json,
+    summarised in profiles/hbm_traffic.md).  Keys starting with "_" are metadata."""
     path = ROOT / "profiles" / "traffic.json"
     if path.exists():
         try:
@@ -259,9 +261,9 @@ def main() -> int:
         "rmsnorm8192": lambda: bench_rmsnorm(8192, steps, warmup),
         "sanaA": lambda: bench_sana(2, 70, 4096, steps, warmup),
         "sanaB": lambda: bench_sana(1, 70, 16384, steps, warmup),
-        "fa_fwd_jvp": lambda: bench_fa("fwd_jvp", max(5, steps // 10), max(2, warmup // 5)),
-        "fa_jvp": lambda: bench_fa("jvp", max(5, steps // 10), max(2, warmup // 5)),
-        "fa_fwd": lambda: bench_fa("fwd", max(5, steps // 10), max(2, warmup // 5)),
+        "fa_fwd_jvp": lambda: bench_fa("fwd_jvp", max(10, steps // 5), max(3, warmup // 2)),
+        "fa_jvp": lambda: bench_fa("jvp", max(10, steps // 5), max(3, warmup // 2)),
+        "fa_fwd": lambda: bench_fa("fwd", max(10, steps // 5), max(3, warmup // 2)),
         "copy": lambda: bench_copy(max(5, steps // 5), 3),
     }
     if args.only:
