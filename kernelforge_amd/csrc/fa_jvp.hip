@@ -16,7 +16,8 @@
 // Tiling.  A workgroup is 8 wavefronts x 16 query rows (128 rows) of one
 // (batch, head), two wavefronts per SIMD so that one wavefront's softmax
 // arithmetic runs while the other's matrix products occupy the MFMA pipe.  It
-// scans the key axis in tiles of 64 keys.  Per tile each wavefront computes
+// scans the key axis in tiles of 64 keys (head dims up to 128; D = 256 uses 4
+// wavefronts, one per SIMD, and tiles of 32 keys: see FaTile).  Per tile each wavefront computes
 // the transposed score blocks S^T = K Q^T with v_mfma_f32_16x16x32 (A = K rows
 // from LDS, B = Q held in registers): lane l owns query row l%16 and keys
 // 16*kb + 4*(l/16) + i of key block kb.  Those accumulators are directly the
@@ -44,10 +45,19 @@ namespace {
 
 enum FaMode { FA_FWD = 0, FA_FWD_JVP = 1, FA_JVP = 2 };
 
-constexpr int kBQ = 128;   // query rows per workgroup
-constexpr int kBK = 64;    // keys per tile
-constexpr int kWaves = 8;  // wavefronts per workgroup (16 query rows each)
-constexpr int kThreads = 64 * kWaves;
+// Workgroup shape per padded head dim.  Up to D = 128: 8 wavefronts x 16
+// query rows, 64-key tiles, two wavefronts per SIMD.  D = 256 doubles the Q and
+// accumulator registers per row: 4 wavefronts x 16 rows, 32-key tiles (the
+// double-buffered K/V/tK/tV tiles still take 128 KiB of LDS), one wavefront
+// per SIMD with its 512 registers.
+template <int DP> struct FaTile {
+    static constexpr int BQ = DP > 128 ? 64 : 128;  // query rows per workgroup
+    static constexpr int BK = DP > 128 ? 32 : 64;   // keys per tile
+    static constexpr int WAVES = BQ / 16;           // 16 query rows each
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int HALVES = BK / 32;          // 32-key halves per tile
+    static constexpr int OCC = DP > 128 ? 1 : 2;    // wavefronts per SIMD
+};
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // lazy rescale step of the rescaling scan (log2)
@@ -77,25 +87,28 @@ struct FaParams {
 // against measured LDS conflict counts) so that neither the ds_read_b128 of a
 // K block (16 consecutive rows at one logical chunk) nor the
 // ds_read_b64_tr_b16 of a V^T operand (8 consecutive rows x an aligned pair of
-// chunks) has bank conflicts; swz depends on row % 16 only.
+// chunks) has bank conflicts; swz depends on row % 16 only.  For 32 chunks
+// (512-byte rows) the 16-chunk map is also conflict-free for both patterns in
+// a 64-bank model of the LDS.
 template <int CH> __device__ __forceinline__ int swz(int r) {
-    if constexpr (CH == 16) return (r & 15) ^ ((r & 1) * 12);
+    if constexpr (CH == 16 || CH == 32) return (r & 15) ^ ((r & 1) * 12);
     else if constexpr (CH == 8) return (r & 7) ^ ((r & 1) << 2);
     else return ((r >> 1) & 1) | ((((r >> 1) ^ (r >> 2)) & 1) << 1);
 }
 
-// Async copy of one [kBK][DP] tile (keys k0.., one kv head) into LDS.  A tile
-// is CH = DP/8 copy instructions of 64 lanes x 16 B; wavefront w issues
-// instructions w, w + kWaves, ...
+// Async copy of one [BK][DP] tile (keys k0.., one kv head) into LDS.  A tile
+// is NI = BK*DP/512 copy instructions of 64 lanes x 16 B (RPI rows each);
+// wavefront w issues instructions w, w + WAVES, ...
 template <typename T, int DP>
 __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_stride, int keys_valid,
                                           int D, int wave, int lane) {
     constexpr int CH = DP / 8;
     constexpr int RPI = 64 / CH;
+    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
 #pragma unroll
-    for (int j = 0; j < (CH + kWaves - 1) / kWaves; ++j) {
-        const int i = wave + j * kWaves;
-        if (CH % kWaves == 0 || i < CH) {
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
             const int row0 = i * RPI;
             const int row = row0 + lane / CH;
             const int chunk = (lane % CH) ^ swz<CH>(row);
@@ -109,9 +122,13 @@ __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_strid
 }
 
 // Byte offset, within a full tile, of the 16-byte chunk lane `lane` copies.
-// The rows a lane copies are wave*RPI + lane/CH plus multiples of
-// kWaves*RPI >= 16, so their swizzle (a function of row % 16) is the same for
-// every instruction and one offset serves them all.
+// The rows a lane copies are wave*RPI + lane/CH plus multiples of WAVES*RPI;
+// when that is a multiple of 16 (full_tile_shortcut), their swizzle (a
+// function of row % 16) is the same for every instruction and one offset
+// serves them all.
+template <int DP> constexpr bool full_tile_shortcut() {
+    return (FaTile<DP>::WAVES * (64 / (DP / 8))) % 16 == 0;
+}
 template <typename T, int DP>
 __device__ __forceinline__ uint32_t full_tile_lane_offset(int64_t row_stride, int wave, int lane) {
     constexpr int CH = DP / 8;
@@ -128,10 +145,12 @@ __device__ __forceinline__ void load_tile_full(T* tile, const T* g, int64_t row_
                                                int wave) {
     constexpr int CH = DP / 8;
     constexpr int RPI = 64 / CH;
+    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
+    static_assert(full_tile_shortcut<DP>(), "one lane offset serves every instruction");
 #pragma unroll
-    for (int j = 0; j < (CH + kWaves - 1) / kWaves; ++j) {
-        const int i = wave + j * kWaves;
-        if (CH % kWaves == 0 || i < CH) {
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
             const int row0 = i * RPI;
             const char* src = reinterpret_cast<const char*>(g + (int64_t)row0 * row_stride) + voff;
             __builtin_amdgcn_global_load_lds(
@@ -225,8 +244,10 @@ __device__ __forceinline__ float row_max4(float x) {
 }
 
 template <typename T, int DP, int MODE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
 void fa_kernel(const FaParams p) {
+    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK, kWaves = FaTile<DP>::WAVES;
     constexpr bool JVP = MODE != FA_FWD;
     constexpr int NT = JVP ? 2 : 1;   // tensors per side: K (, tK) and V (, tV)
     constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
@@ -315,7 +336,7 @@ void fa_kernel(const FaParams p) {
     };
 
     // Full tiles (all 64 keys valid, D == DP) take the uniform-address copy.
-    const uint32_t voff = full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane);
+    const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane) : 0u;
     const bool dense_rows = p.D == DP;
     const T* const kbase = static_cast<const T*>(p.k) + kv_base;
     const T* const vbase = static_cast<const T*>(p.v) + kv_base;
@@ -396,14 +417,16 @@ void fa_kernel(const FaParams p) {
             const T* const s0 = (vs ? vbase : kbase) + off;
             const T* const s1 = (vs ? tvbase : tkbase) + off;
             const bool tan = JVP && (vs ? use_tv : use_tk);
-            if (dense_rows && k0 + kBK <= p.Nk) {
-                load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
-                if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
-            } else {
-                const int kv = p.Nk - k0;
-                load_tile<T, DP>(d0, s0, kv_row_stride, kv, p.D, wave, lane);
-                if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
+            if constexpr (full_tile_shortcut<DP>()) {
+                if (dense_rows && k0 + kBK <= p.Nk) {
+                    load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
+                    if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
+                    return;
+                }
             }
+            const int kv = p.Nk - k0;
+            load_tile<T, DP>(d0, s0, kv_row_stride, kv, p.D, wave, lane);
+            if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
         };
         auto issue = [&](int tile, auto bufc) {
             issue_side(tile, bufc, std::false_type{});
@@ -506,7 +529,7 @@ void fa_kernel(const FaParams p) {
                 __syncthreads();  // tile t resident; every wavefront is done with tile t-1
                 if (t + 1 < ntiles) issue_side(t + 1, nbuf, std::false_type{});
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
                     scores(bufc, h, s, ts);
                     if (h == 0 && t + 1 < ntiles) issue_side(t + 1, nbuf, std::true_type{});
                     if (masked) apply_mask(s, k0, h);
@@ -570,7 +593,7 @@ void fa_kernel(const FaParams p) {
                 wait_vmem();
                 __syncthreads();
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
                     f32x4 s[2], ts[2];
                     u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
                     scores(buf0, h, s, ts);
@@ -617,11 +640,12 @@ int launch_mode(const FaParams& p, int dp, hipStream_t stream) {
         set_error("fa: grid too large");
         return KF_E_UNSUPPORTED;
     }
-    const dim3 grid((unsigned)blocks), block(kThreads);
+    const dim3 grid((unsigned)blocks);
     switch (dp) {
-        case 32: hipLaunchKernelGGL((fa_kernel<T, 32, MODE>), grid, block, 0, stream, p); break;
-        case 64: hipLaunchKernelGGL((fa_kernel<T, 64, MODE>), grid, block, 0, stream, p); break;
-        case 128: hipLaunchKernelGGL((fa_kernel<T, 128, MODE>), grid, block, 0, stream, p); break;
+        case 32: hipLaunchKernelGGL((fa_kernel<T, 32, MODE>), grid, dim3(FaTile<32>::THREADS), 0, stream, p); break;
+        case 64: hipLaunchKernelGGL((fa_kernel<T, 64, MODE>), grid, dim3(FaTile<64>::THREADS), 0, stream, p); break;
+        case 128: hipLaunchKernelGGL((fa_kernel<T, 128, MODE>), grid, dim3(FaTile<128>::THREADS), 0, stream, p); break;
+        case 256: hipLaunchKernelGGL((fa_kernel<T, 256, MODE>), grid, dim3(FaTile<256>::THREADS), 0, stream, p); break;
         default: set_error("fa: head dim %d not supported by this build", p.D); return KF_E_UNSUPPORTED;
     }
     return check_launch("fa_kernel launch");
@@ -639,11 +663,10 @@ int fa_dispatch(int mode, FaParams p, int dtype, hipStream_t stream) {
     if (p.B == 0 || p.Nq == 0) return KF_OK;
     KF_REQUIRE(p.q && p.k && p.v && p.o && p.lse && (mode == FA_FWD || p.to), KF_E_INVALID,
                "fa: null pointer");
-    KF_REQUIRE(p.D <= 128, KF_E_UNSUPPORTED, "fa: head dim %d > 128 is not supported by this build",
-               p.D);
-    const int dp = p.D <= 32 ? 32 : p.D <= 64 ? 64 : 128;
+    const int dp = p.D <= 32 ? 32 : p.D <= 64 ? 64 : p.D <= 128 ? 128 : 256;
+    const int bq = dp > 128 ? FaTile<256>::BQ : FaTile<128>::BQ;
     p.group = p.Hq / p.Hkv;
-    p.n_qtiles = (p.Nq + kBQ - 1) / kBQ;
+    p.n_qtiles = (p.Nq + bq - 1) / bq;
     p.scale_log2 = p.scale * kLog2e;
     if (mode != FA_FWD && p.Nk == 0) {
         // No keys: O = 0 and tO = 0 by the empty-row convention; the kernel

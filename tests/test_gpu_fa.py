@@ -43,6 +43,14 @@ CASES = (
     (1, 23, 37, 2, 2, 80, False, 0.15),
     (1, 999, 515, 2, 2, 64, False, None),
 )
+# Head dims above 128 (the 4-wavefront, 32-key-tile schedule): several key
+# tiles, partial tiles, causal masks, GQA and padded head dims.
+CASES_WIDE = (
+    (1, 130, 97, 2, 1, 256, True, None),
+    (2, 70, 45, 2, 2, 200, False, 0.1),
+    (1, 64, 256, 1, 1, 136, False, None),
+    (1, 200, 200, 4, 2, 256, False, None),
+)
 
 
 def make_inputs(case, dtype, *, noncontiguous=False, seed=2026):
@@ -67,15 +75,9 @@ def double_reference(inputs):
     return tuple(None if x is None else x.detach().cpu().double() for x in inputs)
 
 
-def _skip_unsupported(case):
-    if case[5] > 128:
-        pytest.skip("head dim > 128 is not implemented by the gfx950 kernels yet")
-
-
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("case", CASES + CASES_WIDE)
 def test_standalone_jvp(case, dtype):
-    _skip_unsupported(case)
     q, k, v, tq, tk, tv = make_inputs(case, dtype)
     kwargs = dict(causal=case[-2], softmax_scale=case[-1])
     out, lse = flash_attention(q, k, v, return_lse=True, **kwargs)
@@ -98,10 +100,9 @@ def test_standalone_jvp(case, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("case", CASES + CASES_WIDE)
 def test_fused_forward_jvp(case, dtype):
     """The single-pass (O, LSE, tO) kernel against the fp64 oracle and the two-launch path."""
-    _skip_unsupported(case)
     q, k, v, tq, tk, tv = make_inputs(case, dtype)
     kwargs = dict(causal=case[-2], softmax_scale=case[-1])
     out, lse, tangent = flash_attention_fwd_jvp(q, k, v, tq, tk, tv, **kwargs)
@@ -296,7 +297,8 @@ def test_baseline_config_fused():
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("jump", (30.0, 140.0))
-def test_scores_growing_past_first_tile(dtype, jump):
+@pytest.mark.parametrize("d", (64, 256))
+def test_scores_growing_past_first_tile(dtype, jump, d):
     """Keys after the first tile score `jump` log2 units above it.
 
     The forward kernels fix each row's exponent reference at the max of its
@@ -304,7 +306,7 @@ def test_scores_growing_past_first_tile(dtype, jump):
     2^140 overflows; fp16 overflows already at 2^16.  An overflow must send
     the workgroup to the rescaling scan and still give the oracle's result.
     """
-    b, n, h, d = 1, 300, 2, 64
+    b, n, h = 1, 300, 2
     g = torch.Generator().manual_seed(11)
     q = torch.full((b, n, h, d), 2.0)
     k = 0.05 * torch.randn(b, n, h, d, generator=g)
