@@ -73,6 +73,19 @@ int kf_rmsnorm_fwd(const void* x, const void* weight, void* y,
                    kf_stream_t stream);
 
 /*
+ * kf_rmsnorm_fwd on rows that start every ld_x (input) and ld_y (output)
+ * elements, ld >= dim.  y may equal x with ld_y == ld_x (in place).  Used to
+ * normalise the q and k parts of a packed qkv[B, N, 3, C] buffer in place:
+ * rows = B*N, dim = C, ld = 3*C, x = y = qkv + part*C.  Replaces the q_norm /
+ * k_norm RMSNorm modules of LiteLA.forward (SANA_LinearAttention/
+ * original.py:91-94, 129-130), which normalise over the C channels of each
+ * token; the arithmetic is kf_rmsnorm_fwd's.
+ */
+int kf_rmsnorm_fwd_strided(const void* x, const void* weight, void* y,
+                           int64_t rows, int64_t dim, int64_t ld_x, int64_t ld_y,
+                           float eps, int dtype, kf_stream_t stream);
+
+/*
  * Weight-free fp32 RMSNorm with the two-scan baseline's semantics:
  * b[r, :] = a[r, :] / sqrt(sum_c a[r, c]^2 / n + eps).
  *

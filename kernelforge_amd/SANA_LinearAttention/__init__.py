@@ -1,6 +1,9 @@
-"""SANA ReLU linear attention drop-in (mirrors SANA_LinearAttention/__init__.py:3-26
-for the attention hot path: ``qkv_attn_matmul``)."""
+"""SANA ReLU linear attention drop-in (mirrors SANA_LinearAttention/__init__.py:3-26):
+the attention factory ``qkv_attn_matmul``, the ``LiteLA`` / ``CustomLiteLA`` /
+``JointLiteLA`` modules and the ``qkv_projection`` factory."""
 
 from .custom import default_splits, linear_attention, qkv_attn_matmul
+from .modules import CustomLiteLA, JointLiteLA, LiteLA, qkv_projection
 
-__all__ = ["qkv_attn_matmul", "linear_attention", "default_splits"]
+__all__ = ["LiteLA", "CustomLiteLA", "JointLiteLA", "qkv_attn_matmul", "qkv_projection",
+           "linear_attention", "default_splits"]

@@ -32,6 +32,8 @@ SIGNATURES = {
     "kf_status_string": (ctypes.c_char_p, [_int]),
     "kf_last_error": (ctypes.c_char_p, []),
     "kf_rmsnorm_fwd": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _int, _c_void_p]),
+    "kf_rmsnorm_fwd_strided": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p]),
     "kf_rmsnorm_noweight_f32": (_int, [_c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p]),
     "kf_linattn_default_splits": (_i64, [_i64, _i64, _i64, _i64]),
     "kf_linattn_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),

@@ -21,11 +21,14 @@ namespace {
 
 constexpr int kBlock = 256;  // 4 waves (generic kernel)
 
+// x and y rows start every ld_x / ld_y elements (ld >= dim); the 16-byte
+// vector path needs those strides, like the base pointers, 16-byte aligned.
+// y may alias x (in place, same stride): every row is read whole into
+// registers before any of it is written.
 template <typename T, int VPT, int WPR, int WAVES, bool HAS_W>
-__global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* __restrict__ x,
-                                                                 const T* __restrict__ w,
-                                                                 T* __restrict__ y, int64_t rows,
-                                                                 int dim, float eps) {
+__global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, const T* __restrict__ w,
+                                                                 T* y, int64_t rows, int dim,
+                                                                 int64_t ld_x, int64_t ld_y, float eps) {
     constexpr int VEC = 16 / sizeof(T);
     constexpr int ROWS_PER_BLOCK = WAVES / WPR;
     const int wave = threadIdx.x >> 6;
@@ -36,7 +39,7 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* __rest
     const bool row_ok = row < rows;
     const int nvec = dim / VEC;
 
-    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * (int64_t)dim);
+    const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * ld_x);
     u32x4 xv[VPT];
     float ss = 0.f;
 #pragma unroll
@@ -68,7 +71,7 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* __rest
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
 
     const u32x4* wr = reinterpret_cast<const u32x4*>(w);
-    u32x4* yr = reinterpret_cast<u32x4*>(y + row * (int64_t)dim);
+    u32x4* yr = reinterpret_cast<u32x4*>(y + row * ld_y);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int j = (i * WPR + slice) * 64 + lane;
@@ -94,13 +97,12 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* __rest
 
 // Any dim / alignment: one block per row, two passes over the row.
 template <typename T, bool HAS_W>
-__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const T* __restrict__ x,
-                                                                 const T* __restrict__ w,
-                                                                 T* __restrict__ y, int64_t rows,
-                                                                 int64_t dim, float eps) {
+__global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const T* x, const T* __restrict__ w,
+                                                                 T* y, int64_t rows, int64_t dim,
+                                                                 int64_t ld_x, int64_t ld_y, float eps) {
     const int64_t row = blockIdx.x;
     if (row >= rows) return;
-    const T* xr = x + row * dim;
+    const T* xr = x + row * ld_x;
     float ss = 0.f;
     for (int64_t c = threadIdx.x; c < dim; c += kBlock) {
         const float f = to_f32(xr[c]);
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const T* __rest
     __syncthreads();
     ss = part[0] + part[1] + part[2] + part[3];
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-    T* yr = y + row * dim;
+    T* yr = y + row * ld_y;
     for (int64_t c = threadIdx.x; c < dim; c += kBlock) {
         const T n = from_f32<T>(to_f32(xr[c]) * inv);
         if constexpr (HAS_W)
@@ -123,8 +125,8 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_generic_kernel(const T* __rest
 }
 
 template <typename T, int VPT, int WPR, int WAVES, bool HAS_W>
-int launch_vec(const void* x, const void* w, void* y, int64_t rows, int64_t dim, float eps,
-               hipStream_t stream) {
+int launch_vec(const void* x, const void* w, void* y, int64_t rows, int64_t dim, int64_t ld_x,
+               int64_t ld_y, float eps, hipStream_t stream) {
     static_assert(WAVES % WPR == 0, "a block holds whole rows");
     constexpr int ROWS_PER_BLOCK = WAVES / WPR;
     const int64_t blocks = (rows + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK;
@@ -132,53 +134,63 @@ int launch_vec(const void* x, const void* w, void* y, int64_t rows, int64_t dim,
                (long long)rows);
     hipLaunchKernelGGL((rmsnorm_vec_kernel<T, VPT, WPR, WAVES, HAS_W>), dim3((unsigned)blocks),
                        dim3(64 * WAVES), 0, stream, static_cast<const T*>(x),
-                       static_cast<const T*>(w), static_cast<T*>(y), rows, (int)dim, eps);
+                       static_cast<const T*>(w), static_cast<T*>(y), rows, (int)dim, ld_x, ld_y, eps);
     return check_launch("rmsnorm_vec_kernel launch");
 }
 
 template <typename T, bool HAS_W>
-int dispatch(const void* x, const void* w, void* y, int64_t rows, int64_t dim, float eps,
-             hipStream_t stream) {
+int dispatch(const void* x, const void* w, void* y, int64_t rows, int64_t dim, int64_t ld_x,
+             int64_t ld_y, float eps, hipStream_t stream) {
     if (rows == 0) return KF_OK;
     constexpr int VEC = 16 / sizeof(T);
     const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) &&
-                         (!HAS_W || (uintptr_t)w % 16 == 0) && (dim % VEC == 0);
+                         (!HAS_W || (uintptr_t)w % 16 == 0) && (dim % VEC == 0) &&
+                         (ld_x % VEC == 0) && (ld_y % VEC == 0);
     const int64_t nvec = dim / VEC;
     if (aligned) {
         // (vectors per lane, waves per row, waves per block).
-        if (nvec <= 64) return launch_vec<T, 1, 1, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 128) return launch_vec<T, 2, 1, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 256) return launch_vec<T, 2, 2, 4, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 512) return launch_vec<T, 2, 4, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 1024) return launch_vec<T, 2, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 2048) return launch_vec<T, 4, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
-        if (nvec <= 4096) return launch_vec<T, 8, 8, 8, HAS_W>(x, w, y, rows, dim, eps, stream);
+        if (nvec <= 64) return launch_vec<T, 1, 1, 4, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 128) return launch_vec<T, 2, 1, 4, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 256) return launch_vec<T, 2, 2, 4, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 512) return launch_vec<T, 2, 4, 8, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 1024) return launch_vec<T, 2, 8, 8, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 2048) return launch_vec<T, 4, 8, 8, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
+        if (nvec <= 4096) return launch_vec<T, 8, 8, 8, HAS_W>(x, w, y, rows, dim, ld_x, ld_y, eps, stream);
     }
     KF_REQUIRE(rows <= 0x7fffffff, KF_E_UNSUPPORTED, "rmsnorm: %lld rows exceed the grid limit",
                (long long)rows);
     hipLaunchKernelGGL((rmsnorm_generic_kernel<T, HAS_W>), dim3((unsigned)rows), dim3(kBlock), 0,
                        stream, static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<T*>(y), rows, dim, eps);
+                       static_cast<T*>(y), rows, dim, ld_x, ld_y, eps);
     return check_launch("rmsnorm_generic_kernel launch");
 }
 
 }  // namespace
 }  // namespace kf
 
-extern "C" int kf_rmsnorm_fwd(const void* x, const void* weight, void* y, int64_t rows,
-                              int64_t dim, float eps, int dtype, kf_stream_t stream) {
+extern "C" int kf_rmsnorm_fwd_strided(const void* x, const void* weight, void* y, int64_t rows,
+                                      int64_t dim, int64_t ld_x, int64_t ld_y, float eps, int dtype,
+                                      kf_stream_t stream) {
     using namespace kf;
     KF_REQUIRE(rows >= 0 && dim >= 1, KF_E_INVALID, "rmsnorm: bad shape rows=%lld dim=%lld",
                (long long)rows, (long long)dim);
+    KF_REQUIRE(ld_x >= dim && ld_y >= dim, KF_E_INVALID,
+               "rmsnorm: row strides ld_x=%lld ld_y=%lld must be >= dim=%lld", (long long)ld_x,
+               (long long)ld_y, (long long)dim);
     KF_REQUIRE(rows == 0 || (x && y && weight), KF_E_INVALID, "rmsnorm: null pointer");
     KF_REQUIRE(dim <= 0x7fffffff, KF_E_UNSUPPORTED, "rmsnorm: dim %lld too large", (long long)dim);
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (dtype) {
-        case KF_F32: return dispatch<float, true>(x, weight, y, rows, dim, eps, s);
-        case KF_F16: return dispatch<f16, true>(x, weight, y, rows, dim, eps, s);
-        case KF_BF16: return dispatch<bf16, true>(x, weight, y, rows, dim, eps, s);
+        case KF_F32: return dispatch<float, true>(x, weight, y, rows, dim, ld_x, ld_y, eps, s);
+        case KF_F16: return dispatch<f16, true>(x, weight, y, rows, dim, ld_x, ld_y, eps, s);
+        case KF_BF16: return dispatch<bf16, true>(x, weight, y, rows, dim, ld_x, ld_y, eps, s);
         default: set_error("rmsnorm: unknown dtype %d", dtype); return KF_E_INVALID;
     }
+}
+
+extern "C" int kf_rmsnorm_fwd(const void* x, const void* weight, void* y, int64_t rows,
+                              int64_t dim, float eps, int dtype, kf_stream_t stream) {
+    return kf_rmsnorm_fwd_strided(x, weight, y, rows, dim, dim, dim, eps, dtype, stream);
 }
 
 extern "C" int kf_rmsnorm_noweight_f32(const float* a, float* b, int64_t rows, int64_t n,
@@ -188,5 +200,5 @@ extern "C" int kf_rmsnorm_noweight_f32(const float* a, float* b, int64_t rows, i
                (long long)rows, (long long)n);
     KF_REQUIRE(rows == 0 || (a && b), KF_E_INVALID, "rmsnorm: null pointer");
     KF_REQUIRE(n <= 0x7fffffff, KF_E_UNSUPPORTED, "rmsnorm: n %lld too large", (long long)n);
-    return dispatch<float, false>(a, nullptr, b, rows, n, eps, static_cast<hipStream_t>(stream));
+    return dispatch<float, false>(a, nullptr, b, rows, n, n, n, eps, static_cast<hipStream_t>(stream));
 }

@@ -80,6 +80,41 @@ def rms_norm_tensor(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) ->
     return out
 
 
+def _row_layout(t: torch.Tensor) -> tuple[int, int]:
+    """(rows, row stride) of a tensor whose rows (last dim) are contiguous and
+    evenly spaced, e.g. the q slice ``qkv[:, :, 0]`` of a packed qkv buffer."""
+    if t.stride(-1) != 1:
+        raise ValueError("the last dimension must be contiguous")
+    rows, ld = 1, t.shape[-1]
+    for i in range(t.dim() - 2, -1, -1):
+        if t.shape[i] == 1:
+            continue
+        if rows == 1:
+            ld = t.stride(i)
+        elif t.stride(i) != rows * ld:
+            raise ValueError("rows must be evenly spaced in memory")
+        rows *= t.shape[i]
+    return rows, ld
+
+
+def rms_norm_rows_(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """Normalise every row of x (last dim) in place; x may be a strided view whose
+    rows are evenly spaced, such as the q or k part of a packed ``qkv[B, N, 3, C]``
+    (the LiteLA ``qk_norm`` of SANA_LinearAttention/original.py:91-94, 129-130).
+    Same arithmetic as ``rms_norm`` (rmsnorm/original.py:38, 51-52)."""
+    if x.dim() < 1 or weight.shape != (x.shape[-1],) or weight.dtype != x.dtype:
+        raise ValueError("weight must have shape (x.shape[-1],) and x's dtype")
+    _lib.require_gpu(x, weight)
+    if x.numel() == 0:
+        return x
+    rows, ld = _row_layout(x)
+    weight = weight.contiguous()
+    rc = _lib.load().kf_rmsnorm_fwd_strided(_lib.ptr(x), _lib.ptr(weight), _lib.ptr(x), rows, x.shape[-1],
+                                            ld, ld, float(eps), _lib.kf_dtype(x.dtype), _lib.stream_of(x))
+    _lib.check(rc, "kf_rmsnorm_fwd_strided")
+    return x
+
+
 def original_tilelang_rms_norm(A: torch.Tensor, blk_m: int = 1) -> torch.Tensor:
     """fp32 weight-free RMSNorm with the two-scan baseline's semantics.
 

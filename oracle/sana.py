@@ -79,3 +79,31 @@ def linear_attention_split(qkv: torch.Tensor, heads: int, dim: int, splits: int,
     out = state @ q
     out = out[:, :, :-1] / (out[:, :, -1:] + eps)
     return out.reshape(B, C, N).permute(0, 2, 1).contiguous()
+
+
+def lite_la_forward(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias, proj_weight: torch.Tensor,
+                    proj_bias, heads: int, eps: float = 1e-15, q_norm_weight=None, k_norm_weight=None,
+                    norm_eps: float = 1e-5, qkv_dtype=None) -> torch.Tensor:
+    """``LiteLA.forward`` (SANA_LinearAttention/original.py:119-145) on the CPU.
+
+    ``qkv = x W^T (+ b)`` reshaped to ``[B, N, 3, C]`` (:122-123); the optional
+    q/k RMSNorm over C (:91-94, 129-130, with the rounding points of
+    ``oracle.rmsnorm.rmsnorm``); the fp32 linear attention of ``attn_matmul``
+    (:99-117) on the packed layout (:132-134, 136); ``.to(dtype)`` and the
+    output projection (:138-143).  ``qkv_dtype`` rounds the projected qkv the
+    way a GEMM with a 16-bit output does (fp32 accumulation, one rounding).
+    """
+    from .rmsnorm import rmsnorm
+
+    x = x.detach().cpu()
+    dtype = x.dtype
+    B, N, C = x.shape
+    f = lambda t: None if t is None else t.detach().cpu().float()
+    qkv = torch.nn.functional.linear(x.float(), f(qkv_weight), f(qkv_bias))
+    qkv = qkv.to(qkv_dtype or dtype).reshape(B, N, 3, C)
+    if q_norm_weight is not None:
+        q = rmsnorm(qkv[:, :, 0], q_norm_weight.detach().cpu().to(qkv.dtype), norm_eps)
+        k = rmsnorm(qkv[:, :, 1], k_norm_weight.detach().cpu().to(qkv.dtype), norm_eps)
+        qkv = torch.stack((q, k, qkv[:, :, 2]), dim=2)
+    out = linear_attention(qkv, heads, C // heads, eps).to(dtype)
+    return torch.nn.functional.linear(out.float(), f(proj_weight), f(proj_bias))

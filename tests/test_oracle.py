@@ -125,6 +125,34 @@ def test_mutation_sana_drop_ones_row_or_transpose():
     assert not torch.allclose(bad, ref, rtol=1e-3)
 
 
+def test_lite_la_forward_glue():
+    """LiteLA.forward's glue (part order of the packed qkv, the q/k RMSNorm, the
+    output projection) on top of the golden-pinned linear attention: with
+    W_qkv = [I; 2I; 3I] the packed qkv is exactly (x, 2x, 3x), a proj of
+    diag(d) + b scales and shifts the attention output per channel."""
+    g = torch.Generator().manual_seed(5)
+    B, N, H, D = 2, 40, 3, 8
+    C = H * D
+    x = torch.randn(B, N, C, generator=g, dtype=torch.float64).float()
+    eye = torch.eye(C)
+    w_qkv = torch.cat([eye, 2 * eye, 3 * eye])
+    d = torch.rand(C, generator=g) + 0.5
+    bias = torch.randn(C, generator=g)
+    got = osana.lite_la_forward(x, w_qkv, None, torch.diag(d), bias, H, 1e-15)
+    att = osana.linear_attention(torch.stack((x, 2 * x, 3 * x), dim=2), H, D)
+    torch.testing.assert_close(got, att * d + bias, rtol=1e-6, atol=1e-6)
+    # a swapped q/v order is caught
+    swapped = osana.linear_attention(torch.stack((3 * x, 2 * x, x), dim=2), H, D)
+    assert not torch.allclose(swapped * d + bias, got, rtol=1e-3)
+    # qk_norm normalises q and k over C before the attention
+    wq, wk = torch.rand(C, generator=g) + 0.5, torch.rand(C, generator=g) + 0.5
+    got = osana.lite_la_forward(x, w_qkv, None, torch.diag(d), bias, H, 1e-15, wq, wk, 1e-5)
+    qn = orms.rmsnorm(x, wq, 1e-5)
+    kn = orms.rmsnorm(2 * x, wk, 1e-5)
+    att = osana.linear_attention(torch.stack((qn, kn, 3 * x), dim=2), H, D)
+    torch.testing.assert_close(got, att * d + bias, rtol=1e-6, atol=1e-6)
+
+
 # ---------------------------------------------------------------------------
 # FlashAttention forward / JVP
 # ---------------------------------------------------------------------------
