@@ -6,8 +6,8 @@ algorithmic traffic (read x once, write y once, read w).  The same line
 carries, under "results", every BASELINE config measured the same way:
 the RMSNorm hidden sweep {2048, 4096, 8192}, SANA linear attention at both
 shapes (HBM GB/s and TFLOP/s), and FlashAttention at B=2, H=16, N=4096,
-D=128 (fused forward+JVP, standalone JVP from LSE, forward), in TFLOP/s
-against the bf16 dense MFMA peak.
+D=128 (fused forward+JVP, standalone JVP from LSE, forward, backward), in
+TFLOP/s against the bf16 dense MFMA peak.
 
 Timing: inputs are resident in HBM before the timed region; input/output
 sets rotate so that the bytes touched between two uses of a buffer exceed
@@ -150,6 +150,20 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
         _lib.check(rc, "kf_fa_fwd")
         fnc, a = lib.kf_fa_jvp, (*P, *dims)
         gemms, name = 6, "fa_kernel<bf16,128,JVP>"
+    elif mode == "bwd":
+        # Backward from the forward's O and LSE: dq kernel + dkdv kernel.  The
+        # algorithmic count is the usual 5 GEMM-equivalents (S recomputed
+        # once, dP, dV, dK, dQ); the kernels recompute S and dP twice.
+        rc = lib.kf_fa_fwd(P[0], P[1], P[2], P[6], P[7], *dims)
+        _lib.check(rc, "kf_fa_fwd")
+        dout = torch.randn(shape, generator=g).to(torch.bfloat16).to("cuda")
+        grads = [torch.empty_like(x) for x in (q, k, v)]
+        ws_bytes = lib.kf_fa_bwd_workspace_bytes(B, N, H, D)
+        ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
+        fnc = lib.kf_fa_bwd
+        a = (P[0], P[1], P[2], P[6], P[7], _lib.ptr(dout), *(_lib.ptr(x) for x in grads), _lib.ptr(ws),
+             ws_bytes, *dims)
+        gemms, name = 5, "fa_bwd_dq_kernel+fa_bwd_dkdv_kernel<bf16,128>"
     else:
         fnc, a = lib.kf_fa_fwd, (P[0], P[1], P[2], P[6], P[7], *dims)
         gemms, name = 2, "fa_kernel<bf16,128,FWD>"
@@ -242,7 +256,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
-                         "fa_fwd_jvp|fa_jvp|fa_fwd|copy), e.g. under rocprofv3")
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|copy), e.g. under rocprofv3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -264,6 +278,7 @@ def main() -> int:
         "fa_fwd_jvp": lambda: bench_fa("fwd_jvp", max(10, steps // 5), max(3, warmup // 2)),
         "fa_jvp": lambda: bench_fa("jvp", max(10, steps // 5), max(3, warmup // 2)),
         "fa_fwd": lambda: bench_fa("fwd", max(10, steps // 5), max(3, warmup // 2)),
+        "fa_bwd": lambda: bench_fa("bwd", max(10, steps // 5), max(3, warmup // 2)),
         "copy": lambda: bench_copy(max(5, steps // 5), 3),
     }
     if args.only:

@@ -187,6 +187,29 @@ int kf_fa_fwd_jvp(const void* q, const void* k, const void* v,
                   int64_t D, float scale, int causal, int dtype,
                   kf_stream_t stream);
 
+/*
+ * Workspace bytes kf_fa_bwd needs (fp32 per-row statistics, rows padded to
+ * the kernel's query tile); -1 for an invalid shape.
+ */
+int64_t kf_fa_bwd_workspace_bytes(int64_t B, int64_t Nq, int64_t Hq, int64_t D);
+
+/*
+ * Gradients dq, dk, dv (layouts of q, k, v) of the attention output for the
+ * output cotangent dout [B, Nq, Hq, D], from the forward's o and natural-log
+ * lse (P = exp(scale*q k^T - lse), recomputed; +inf rows contribute 0):
+ *   Delta = rowsum(dout * o),  dS = P * (dout v^T - Delta),
+ *   dq = scale*dS k,  dk = scale*dS^T q,  dv = P^T dout,
+ * dk/dv summed over the query heads of each KV head.  Deterministic (no
+ * atomics).  workspace: at least kf_fa_bwd_workspace_bytes, device memory.
+ * Replaces flash-attn's _flash_attn_backward as called by
+ * FlashAttentionFunction.backward (flash_attention_jvp/custom.py:252-267).
+ */
+int kf_fa_bwd(const void* q, const void* k, const void* v, const void* o,
+              const float* lse, const void* dout, void* dq, void* dk, void* dv,
+              void* workspace, int64_t workspace_bytes,
+              int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv,
+              int64_t D, float scale, int causal, int dtype, kf_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,13 @@ SIGNATURES = {
          _c_void_p, _c_void_p, _c_void_p,
          _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p],
     ),
+    "kf_fa_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "kf_fa_bwd": (
+        _int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p],
+    ),
 }
 
 _lock = threading.Lock()

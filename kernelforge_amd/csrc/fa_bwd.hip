@@ -1,0 +1,522 @@
+// FlashAttention backward (vector-Jacobian product) for gfx950.
+//
+// Semantics: the reverse-mode derivative of dense softmax attention
+// (flash_attention_jvp/original.py:6-30) that the reference obtains from
+// flash-attn's _flash_attn_backward (flash_attention_jvp/custom.py:252-267):
+//   P = exp(scale q k^T - LSE),  Delta_i = sum_d dO_id O_id,
+//   dP = dO v^T,  dS = P * (dP - Delta),
+//   dQ = scale dS k,  dK = scale dS^T q,  dV = P^T dO,
+// with dK and dV summed over the query heads that share a KV head (GQA/MQA).
+// P is recomputed from the forward's natural-log LSE; rows with LSE = +inf
+// (no valid key) get P = 0 and contribute nothing.
+//
+// Two launches, no atomics, deterministic:
+//   1. dq kernel, one workgroup per (query tile, batch, query head), shaped
+//      like the forward: lane l owns query row l%16 and computes S^T = K Q^T
+//      and dP^T = V dO^T over K/V tiles streamed through LDS, then
+//      dQ^T += K^T dS^T with K^T read by transposing LDS reads.  It also
+//      writes Delta and LSE*log2(e) of its rows to the workspace.
+//   2. dkdv kernel, one workgroup per (key tile, batch, KV head): K and V of
+//      its keys stay in registers, lane l owns key l%16; it streams the Q and
+//      dO tiles (plus their LSE/Delta entries) of every query head of the
+//      group, in a fixed order, computes S = Q K^T and dP = dO V^T with the
+//      key as the output column, and accumulates dV^T += dO^T P and
+//      dK^T += Q^T dS with dO^T and Q^T read by transposing LDS reads.
+// Both products of the pair are v_mfma_f32_16x16x32 with the same operand
+// enumeration as the forward: the score accumulators of two 16-row blocks
+// are directly the B operand of the next product once packed to 16 bits.
+#include "fa_common.h"
+
+namespace kf {
+namespace {
+
+struct FaBwdParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* o;
+    const float* lse;
+    const void* dout;
+    void* dq;
+    void* dk;
+    void* dv;
+    float* ws_lse2;   // [B][Hq][nq_pad]: LSE * log2(e), +inf for rows >= Nq
+    float* ws_delta;  // [B][Hq][nq_pad]: Delta, 0 for rows >= Nq
+    int B, Nq, Nk, Hq, Hkv, D, group;
+    int n_qtiles;  // query tiles of FaTile::BQ rows (dq grid)
+    int n_ktiles;  // key tiles of FaTile::BQ keys (dkdv grid)
+    int nq_pad;    // n_qtiles * FaTile::BQ
+    float scale;
+    float scale_log2;
+    int causal;
+};
+
+// XCD-aware renumbering: the hardware sends block i to XCD i % 8; give each
+// XCD a contiguous range of logical blocks (consecutive tiles of one head,
+// which share K/V or Q/dO rows in that XCD's L2).
+__device__ __forceinline__ int xcd_logical_block() {
+    const int nblk = gridDim.x, id = blockIdx.x;
+    const int per = nblk >> 3, rem = nblk & 7, xcd = id & 7, slot = id >> 3;
+    return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+// Loads 8 consecutive elements of a row as an MFMA B operand (zero if !ok).
+template <typename T>
+__device__ __forceinline__ typename V<T>::x8 load_row8(const T* p, bool ok) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    return __builtin_bit_cast(typename V<T>::x8, ok ? *reinterpret_cast<const u32x4*>(p) : z);
+}
+
+// ---------------------------------------------------------------------------
+// dQ (and the per-row Delta / LSE*log2e workspace).
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
+void fa_bwd_dq_kernel(const FaBwdParams p) {
+    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK;
+    constexpr int DS = DP / 32, DB = DP / 16;
+    typedef typename V<T>::x8 x8;
+    // Double-buffered K and V tiles, one LDS variable per buffer so that the
+    // copies into one buffer are not ordered against reads of the other.
+    __shared__ __attribute__((aligned(16))) T kt0[kBK * DP];
+    __shared__ __attribute__((aligned(16))) T kt1[kBK * DP];
+    __shared__ __attribute__((aligned(16))) T vt0[kBK * DP];
+    __shared__ __attribute__((aligned(16))) T vt1[kBK * DP];
+    auto lds_tile = [&](auto bufc, auto vsc) -> T* {
+        constexpr int buf = decltype(bufc)::value;
+        if constexpr (decltype(vsc)::value)
+            return buf == 0 ? vt0 : vt1;
+        else
+            return buf == 0 ? kt0 : kt1;
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 4;
+
+    const int logical = xcd_logical_block();
+    int qtile = logical % p.n_qtiles;
+    const int rest = logical / p.n_qtiles;
+    const int hq = rest % p.Hq, b = rest / p.Hq;
+    if (p.causal) qtile = p.n_qtiles - 1 - qtile;  // longest scans first
+    const int hk = hq / p.group;
+
+    const int q0w = qtile * kBQ + wave * 16;
+    const int qr = q0w + (lane & 15);
+    const bool row_ok = qr < p.Nq;
+    const int64_t q_row_stride = (int64_t)p.Hq * p.D;
+    const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
+    const int64_t q_off = ((int64_t)b * p.Nq + qr) * q_row_stride + (int64_t)hq * p.D;
+    const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
+    const int diag = p.Nk - p.Nq;
+
+    // Q and dO as B operands (lane: row qr, d = 32*ds + 8*grp + 0..7), and
+    // this lane's share of Delta = dO . O.
+    x8 qreg[DS], doreg[DS];
+    float dot = 0.f;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+        const int d = 32 * ds + 8 * grp;
+        const bool ok = row_ok && d < p.D;
+        qreg[ds] = load_row8(static_cast<const T*>(p.q) + q_off + d, ok);
+        doreg[ds] = load_row8(static_cast<const T*>(p.dout) + q_off + d, ok);
+        const x8 ov = load_row8(static_cast<const T*>(p.o) + q_off + d, ok);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dot = fmaf((float)doreg[ds][j], (float)ov[j], dot);
+    }
+    const float delta = row_sum4(dot);
+    const float lse2 = row_ok ? p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : __builtin_inff();
+    if (grp == 0) {
+        const int64_t w = ((int64_t)b * p.Hq + hq) * p.nq_pad + qr;
+        p.ws_lse2[w] = lse2;
+        p.ws_delta[w] = delta;
+    }
+
+    int key_stop = p.Nk;
+    if (p.causal) key_stop = min(p.Nk, max(0, qtile * kBQ + kBQ + diag));
+    const int ntiles = (key_stop + kBK - 1) / kBK;
+    const int klim = p.causal ? min(p.Nk - 1, qr + diag) : p.Nk - 1;
+    const float c = p.scale_log2;
+    const float nlse2 = -lse2;
+
+    const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane) : 0u;
+    const bool dense_rows = p.D == DP;
+    const T* const kbase = static_cast<const T*>(p.k) + kv_base;
+    const T* const vbase = static_cast<const T*>(p.v) + kv_base;
+
+    auto issue_side = [&](int tile, auto bufc, auto vsc) {
+        const int k0 = tile * kBK;
+        T* const dst = lds_tile(bufc, vsc);
+        const T* const src = (decltype(vsc)::value ? vbase : kbase) + (int64_t)k0 * kv_row_stride;
+        if constexpr (full_tile_shortcut<DP>()) {
+            if (dense_rows && k0 + kBK <= p.Nk) {
+                load_tile_full<T, DP>(dst, src, kv_row_stride, voff, wave);
+                return;
+            }
+        }
+        load_tile<T, DP>(dst, src, kv_row_stride, p.Nk - k0, p.D, wave, lane);
+    };
+
+    f32x4 dq[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dq[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto step = [&](int t, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const std::integral_constant<int, buf ^ 1> nbuf;
+        const int k0 = t * kBK;
+        const bool masked = (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
+        const T* Kt = lds_tile(bufc, std::false_type{});
+        const T* Vt = lds_tile(bufc, std::true_type{});
+        wait_vmem();
+        __syncthreads();  // tile t resident; every wavefront is done with tile t-1
+        if (t + 1 < ntiles) {
+            issue_side(t + 1, nbuf, std::false_type{});
+            issue_side(t + 1, nbuf, std::true_type{});
+        }
+#pragma unroll
+        for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
+            f32x4 s[2], dp[2];
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+                s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int krow = 16 * (2 * h + i2) + (lane & 15);
+#pragma unroll
+                for (int ds = 0; ds < DS; ++ds) {
+                    s[i2] = mfma16x16x32(row_chunk<T, DP>(Kt, krow, 4 * ds + grp), qreg[ds], s[i2]);
+                    dp[i2] = mfma16x16x32(row_chunk<T, DP>(Vt, krow, 4 * ds + grp), doreg[ds], dp[i2]);
+                }
+            }
+            if (masked) {
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (k0 + 16 * (2 * h + i2) + 4 * grp + i > klim) s[i2][i] = -__builtin_inff();
+            }
+            // dS = P (dP - Delta), packed to 16 bits as the B operand of
+            // dQ^T += K^T dS^T (keys 4*grp+0..3 of blocks 2h, 2h+1).
+            u32x2 sw[2];
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float p0 = fast_exp2(fmaf(s[i2][2 * j], c, nlse2));
+                    const float p1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nlse2));
+                    sw[i2][j] = Pk<T>::cvt(p0 * (dp[i2][2 * j] - delta), p1 * (dp[i2][2 * j + 1] - delta));
+                }
+            const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
+#pragma unroll
+            for (int db = 0; db < DB; ++db) dq[db] = mfma16x16x32(vt_operand<T, DP>(Kt, h, db, lane), sb, dq[db]);
+        }
+    };
+    if (ntiles > 0) {
+        issue_side(0, std::integral_constant<int, 0>{}, std::false_type{});
+        issue_side(0, std::integral_constant<int, 0>{}, std::true_type{});
+    }
+    for (int t = 0; t < ntiles; t += 2) {
+        step(t, std::integral_constant<int, 0>{});
+        if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+    }
+
+    // dQ = scale * dS K; lane holds row qr, d = 16*db + 4*grp + 0..3.
+    T* const dqrow = static_cast<T*>(p.dq) + q_off;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const int d = 16 * db + 4 * grp;
+        if (row_ok && d < p.D) {
+            typename V<T>::x4 r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = (T)(dq[db][e] * p.scale);
+            *reinterpret_cast<typename V<T>::x4*>(dqrow + d) = r;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV: one workgroup per FaTile::BQ keys of one KV head, 16 keys per
+// wavefront, scanning query tiles of FaTile::BK rows of every query head of
+// the group.
+// ---------------------------------------------------------------------------
+template <typename T, int DP>
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
+void fa_bwd_dkdv_kernel(const FaBwdParams p) {
+    constexpr int kBKEYS = FaTile<DP>::BQ;  // keys per workgroup
+    constexpr int kBR = FaTile<DP>::BK;     // query rows per tile
+    constexpr int DS = DP / 32, DB = DP / 16;
+    typedef typename V<T>::x8 x8;
+    static_assert(FaTile<DP>::WAVES >= 2, "waves 0 and 1 copy the row statistics");
+    static_assert(kBR <= 64, "one 64-lane copy holds a tile's row statistics");
+    // Double-buffered Q and dO tiles and their rows' [LSE*log2e, Delta].
+    __shared__ __attribute__((aligned(16))) T qt0[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T qt1[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T ot0[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T ot1[kBR * DP];
+    __shared__ __attribute__((aligned(16))) float rs0[2][64];
+    __shared__ __attribute__((aligned(16))) float rs1[2][64];
+    auto lds_tile = [&](auto bufc, auto osc) -> T* {
+        constexpr int buf = decltype(bufc)::value;
+        if constexpr (decltype(osc)::value)
+            return buf == 0 ? ot0 : ot1;
+        else
+            return buf == 0 ? qt0 : qt1;
+    };
+    auto lds_stats = [&](auto bufc, int i) -> float* {
+        return decltype(bufc)::value == 0 ? rs0[i] : rs1[i];
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 4;
+
+    const int logical = xcd_logical_block();
+    const int ktile = logical % p.n_ktiles;
+    const int rest = logical / p.n_ktiles;
+    const int hk = rest % p.Hkv, b = rest / p.Hkv;
+
+    const int k0 = ktile * kBKEYS;             // first key of the workgroup
+    const int k0w = k0 + wave * 16;            // first key of this wavefront
+    const int kr = k0w + (lane & 15);          // this lane's key
+    const bool key_ok = kr < p.Nk;
+    const int64_t q_row_stride = (int64_t)p.Hq * p.D;
+    const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
+    const int64_t kv_off = ((int64_t)b * p.Nk + kr) * kv_row_stride + (int64_t)hk * p.D;
+    const int diag = p.Nk - p.Nq;  // key j valid for query i iff j <= i + diag
+
+    // K and V as B operands (lane: key kr, d = 32*ds + 8*grp + 0..7).
+    x8 kreg[DS], vreg[DS];
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+        const int d = 32 * ds + 8 * grp;
+        const bool ok = key_ok && d < p.D;
+        kreg[ds] = load_row8(static_cast<const T*>(p.k) + kv_off + d, ok);
+        vreg[ds] = load_row8(static_cast<const T*>(p.v) + kv_off + d, ok);
+    }
+
+    // Query tiles: causal masks skip the rows before the first one that sees
+    // key k0; the same range repeats for each query head of the group.
+    const int n_rt = (p.Nq + kBR - 1) / kBR;
+    const int rt0 = p.causal ? min(n_rt, max(0, k0 - diag) / kBR) : 0;
+    const int per_head = n_rt - rt0;
+    const int ntiles = per_head * p.group;
+    const float c = p.scale_log2;
+
+    const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(q_row_stride, wave, lane) : 0u;
+    const bool dense_rows = p.D == DP;
+
+    auto tile_head = [&](int u) { return u / per_head; };
+    auto tile_row0 = [&](int u) { return (rt0 + u % per_head) * kBR; };
+
+    auto issue = [&](int u, auto bufc) {
+        const int hq = hk * p.group + tile_head(u);
+        const int r0 = tile_row0(u);
+        const int64_t off = ((int64_t)b * p.Nq + r0) * q_row_stride + (int64_t)hq * p.D;
+        const T* const qsrc = static_cast<const T*>(p.q) + off;
+        const T* const osrc = static_cast<const T*>(p.dout) + off;
+        T* const qdst = lds_tile(bufc, std::false_type{});
+        T* const odst = lds_tile(bufc, std::true_type{});
+        bool done = false;
+        if constexpr (full_tile_shortcut<DP>()) {
+            if (dense_rows && r0 + kBR <= p.Nq) {
+                load_tile_full<T, DP>(qdst, qsrc, q_row_stride, voff, wave);
+                load_tile_full<T, DP>(odst, osrc, q_row_stride, voff, wave);
+                done = true;
+            }
+        }
+        if (!done) {
+            load_tile<T, DP>(qdst, qsrc, q_row_stride, p.Nq - r0, p.D, wave, lane);
+            load_tile<T, DP>(odst, osrc, q_row_stride, p.Nq - r0, p.D, wave, lane);
+        }
+        // Row statistics of the tile: rows r0 .. r0+kBR-1 lie below nq_pad.
+        if (wave < 2 && (kBR == 64 || lane < kBR)) {
+            const float* src = (wave == 0 ? p.ws_lse2 : p.ws_delta) +
+                               ((int64_t)b * p.Hq + hq) * p.nq_pad + r0 + lane;
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)lds_stats(bufc, wave), 4, 0, 0);
+        }
+    };
+
+    f32x4 dk[DB], dv[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        dk[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dv[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    auto step = [&](int u, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const std::integral_constant<int, buf ^ 1> nbuf;
+        const int r0 = tile_row0(u);
+        // Some (row, key) pair of this wavefront is masked out.
+        const bool masked = p.causal && k0w + 15 > r0 + diag;
+        const T* Qt = lds_tile(bufc, std::false_type{});
+        const T* Ot = lds_tile(bufc, std::true_type{});
+        const float* lse2v = lds_stats(bufc, 0);
+        const float* deltav = lds_stats(bufc, 1);
+        wait_vmem();
+        __syncthreads();  // tile u resident; every wavefront is done with tile u-1
+        if (u + 1 < ntiles) issue(u + 1, nbuf);
+#pragma unroll
+        for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
+            // S and dP for rows 16*(2h+i2) + 4*grp + i of the tile, key kr.
+            f32x4 s[2], dp[2];
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+                s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int row = 16 * (2 * h + i2) + (lane & 15);
+#pragma unroll
+                for (int ds = 0; ds < DS; ++ds) {
+                    s[i2] = mfma16x16x32(row_chunk<T, DP>(Qt, row, 4 * ds + grp), kreg[ds], s[i2]);
+                    dp[i2] = mfma16x16x32(row_chunk<T, DP>(Ot, row, 4 * ds + grp), vreg[ds], dp[i2]);
+                }
+            }
+            u32x2 pw[2], sw[2];
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+                const int rl = 16 * (2 * h + i2) + 4 * grp;
+                const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
+                const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + rl);
+                float pr[4], dsv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float e = fast_exp2(fmaf(s[i2][i], c, -l2[i]));
+                    if (masked && kr > r0 + rl + i + diag) e = 0.f;
+                    pr[i] = e;
+                    dsv[i] = e * (dp[i2][i] - dl[i]);
+                }
+                pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
+                pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
+                sw[i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
+                sw[i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
+            }
+            const x8 pb = __builtin_bit_cast(x8, u32x4{pw[0][0], pw[0][1], pw[1][0], pw[1][1]});
+            const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                dv[db] = mfma16x16x32(vt_operand<T, DP>(Ot, h, db, lane), pb, dv[db]);
+                dk[db] = mfma16x16x32(vt_operand<T, DP>(Qt, h, db, lane), sb, dk[db]);
+            }
+        }
+    };
+    if (ntiles > 0) issue(0, std::integral_constant<int, 0>{});
+    for (int u = 0; u < ntiles; u += 2) {
+        step(u, std::integral_constant<int, 0>{});
+        if (u + 1 < ntiles) step(u + 1, std::integral_constant<int, 1>{});
+    }
+
+    // dK = scale * dS^T Q, dV = P^T dO; lane holds key kr, d = 16*db + 4*grp + 0..3.
+    T* const dkrow = static_cast<T*>(p.dk) + kv_off;
+    T* const dvrow = static_cast<T*>(p.dv) + kv_off;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const int d = 16 * db + 4 * grp;
+        if (key_ok && d < p.D) {
+            typename V<T>::x4 rk, rv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                rk[e] = (T)(dk[db][e] * p.scale);
+                rv[e] = (T)dv[db][e];
+            }
+            *reinterpret_cast<typename V<T>::x4*>(dkrow + d) = rk;
+            *reinterpret_cast<typename V<T>::x4*>(dvrow + d) = rv;
+        }
+    }
+}
+
+template <int DP> int64_t nq_pad_of(int64_t Nq) {
+    return (Nq + FaTile<DP>::BQ - 1) / FaTile<DP>::BQ * FaTile<DP>::BQ;
+}
+
+int64_t padded_rows(int64_t Nq, int64_t D) {
+    return D > 128 ? nq_pad_of<256>(Nq) : nq_pad_of<128>(Nq);
+}
+
+template <typename T, int DP>
+int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
+    const int64_t qblocks = (int64_t)p.n_qtiles * p.Hq * p.B;
+    const int64_t kblocks = (int64_t)p.n_ktiles * p.Hkv * p.B;
+    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff) {
+        set_error("fa_bwd: grid too large");
+        return KF_E_UNSUPPORTED;
+    }
+    if (qblocks > 0) {
+        hipLaunchKernelGGL((fa_bwd_dq_kernel<T, DP>), dim3((unsigned)qblocks), dim3(FaTile<DP>::THREADS), 0,
+                           stream, p);
+        const int rc = check_launch("fa_bwd_dq_kernel launch");
+        if (rc != KF_OK) return rc;
+    }
+    if (kblocks > 0) {
+        hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP>), dim3((unsigned)kblocks), dim3(FaTile<DP>::THREADS), 0,
+                           stream, p);
+        return check_launch("fa_bwd_dkdv_kernel launch");
+    }
+    return KF_OK;
+}
+
+template <typename T>
+int launch_bwd_dp(const FaBwdParams& p, int dp, hipStream_t stream) {
+    switch (dp) {
+        case 32: return launch_bwd<T, 32>(p, stream);
+        case 64: return launch_bwd<T, 64>(p, stream);
+        case 128: return launch_bwd<T, 128>(p, stream);
+        case 256: return launch_bwd<T, 256>(p, stream);
+        default: set_error("fa_bwd: head dim %d not supported by this build", p.D); return KF_E_UNSUPPORTED;
+    }
+}
+
+bool bwd_dims_fit(int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D) {
+    const int64_t lim = 0x3fffffff;
+    return B >= 0 && Nq >= 0 && Nk >= 0 && B <= lim && Nq <= lim && Nk <= lim && Hq <= lim &&
+           Hkv <= lim && D <= lim;
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int64_t kf_fa_bwd_workspace_bytes(int64_t B, int64_t Nq, int64_t Hq, int64_t D) {
+    using namespace kf;
+    if (B < 0 || Nq < 0 || Hq <= 0 || D <= 0 || D > 256 || !bwd_dims_fit(B, Nq, 0, Hq, 1, D)) return -1;
+    return 2 * (int64_t)sizeof(float) * B * Hq * padded_rows(Nq, D);
+}
+
+extern "C" int kf_fa_bwd(const void* q, const void* k, const void* v, const void* o,
+                         const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                         void* workspace, int64_t workspace_bytes, int64_t B, int64_t Nq,
+                         int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D, float scale, int causal,
+                         int dtype, kf_stream_t stream) {
+    using namespace kf;
+    KF_REQUIRE(bwd_dims_fit(B, Nq, Nk, Hq, Hkv, D), KF_E_INVALID, "fa_bwd: shape out of range");
+    KF_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, KF_E_INVALID, "fa_bwd: Hq must be a positive multiple of Hkv");
+    KF_REQUIRE(D > 0 && D % 8 == 0 && D <= 256, KF_E_INVALID,
+               "fa_bwd: head dim must be a positive multiple of 8 <= 256, got %lld", (long long)D);
+    KF_REQUIRE(scale > 0.f && scale < __builtin_inff(), KF_E_INVALID, "fa_bwd: scale must be finite and positive");
+    KF_REQUIRE(dtype == KF_F16 || dtype == KF_BF16, KF_E_INVALID, "fa_bwd: dtype must be f16 or bf16");
+    if (B == 0 || (Nq == 0 && Nk == 0)) return KF_OK;
+    const int64_t need = kf_fa_bwd_workspace_bytes(B, Nq, Hq, D);
+    KF_REQUIRE(need >= 0 && workspace_bytes >= need && (need == 0 || workspace), KF_E_WORKSPACE,
+               "fa_bwd: workspace of %lld bytes needed, %lld given", (long long)need,
+               (long long)workspace_bytes);
+    KF_REQUIRE(q && k && v && o && lse && dout && dq && dk && dv, KF_E_INVALID, "fa_bwd: null pointer");
+    FaBwdParams p{};
+    p.q = q; p.k = k; p.v = v; p.o = o; p.lse = lse; p.dout = dout;
+    p.dq = dq; p.dk = dk; p.dv = dv;
+    const int64_t nq_pad = padded_rows(Nq, D);
+    p.ws_lse2 = static_cast<float*>(workspace);
+    p.ws_delta = static_cast<float*>(workspace) + B * Hq * nq_pad;
+    p.B = (int)B; p.Nq = (int)Nq; p.Nk = (int)Nk; p.Hq = (int)Hq; p.Hkv = (int)Hkv; p.D = (int)D;
+    p.group = (int)(Hq / Hkv);
+    const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
+    const int bq = dp > 128 ? FaTile<256>::BQ : FaTile<128>::BQ;
+    p.n_qtiles = (int)((Nq + bq - 1) / bq);
+    p.n_ktiles = (int)((Nk + bq - 1) / bq);
+    p.nq_pad = (int)nq_pad;
+    p.scale = scale;
+    p.scale_log2 = scale * kLog2e;
+    p.causal = causal ? 1 : 0;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    return dtype == KF_BF16 ? launch_bwd_dp<bf16>(p, dp, s) : launch_bwd_dp<f16>(p, dp, s);
+}

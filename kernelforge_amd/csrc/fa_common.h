@@ -1,0 +1,215 @@
+// Device helpers shared by the FlashAttention kernels (forward / JVP in
+// fa_jvp.hip, backward in fa_bwd.hip) for gfx950: workgroup shapes, the
+// HBM -> LDS tile copies (global_load_lds), the XOR chunk swizzle and the LDS
+// operand reads for v_mfma_f32_16x16x32, and 16-lane-group row reductions.
+#pragma once
+
+#include <type_traits>
+
+#include "kf_common.h"
+
+namespace kf {
+namespace {
+
+enum FaMode { FA_FWD = 0, FA_FWD_JVP = 1, FA_JVP = 2 };
+
+// Workgroup shape per padded head dim.  Up to D = 128: 8 wavefronts x 16
+// query rows, 64-key tiles, two wavefronts per SIMD.  D = 256 doubles the Q and
+// accumulator registers per row: 4 wavefronts x 16 rows, 32-key tiles (the
+// double-buffered K/V/tK/tV tiles still take 128 KiB of LDS), one wavefront
+// per SIMD with its 512 registers.
+template <int DP> struct FaTile {
+    static constexpr int BQ = DP > 128 ? 64 : 128;  // query rows per workgroup
+    static constexpr int BK = DP > 128 ? 32 : 64;   // keys per tile
+    static constexpr int WAVES = BQ / 16;           // 16 query rows each
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int HALVES = BK / 32;          // 32-key halves per tile
+    static constexpr int OCC = DP > 128 ? 1 : 2;    // wavefronts per SIMD
+};
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kRescaleThreshold = 8.0f;  // lazy rescale step of the rescaling scan (log2)
+
+// 256 bytes of zeros in global memory: the source of lanes whose chunk is
+// outside the tensor (key rows >= Nk, head-dim padding).
+__device__ __attribute__((aligned(16))) unsigned g_zero16[64];
+
+struct FaParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* tq;
+    const void* tk;
+    const void* tv;
+    void* o;      // output (FWD, FWD_JVP) or cached input (JVP)
+    float* lse;   // output (FWD, FWD_JVP) or cached input (JVP)
+    void* to;     // output (FWD_JVP, JVP)
+    int B, Nq, Nk, Hq, Hkv, D, group, n_qtiles;
+    float scale;       // natural units
+    float scale_log2;  // scale * log2(e)
+    int causal;
+};
+
+// Physical 16-byte chunk = logical chunk ^ swz(row), for CH chunks per row.
+// Chosen (by enumerating the XOR-linear maps of row % 16 and checking them
+// against measured LDS conflict counts) so that neither the ds_read_b128 of a
+// K block (16 consecutive rows at one logical chunk) nor the
+// ds_read_b64_tr_b16 of a V^T operand (8 consecutive rows x an aligned pair of
+// chunks) has bank conflicts; swz depends on row % 16 only.  For 32 chunks
+// (512-byte rows) the 16-chunk map is also conflict-free for both patterns in
+// a 64-bank model of the LDS.
+template <int CH> __device__ __forceinline__ int swz(int r) {
+    if constexpr (CH == 16 || CH == 32) return (r & 15) ^ ((r & 1) * 12);
+    else if constexpr (CH == 8) return (r & 7) ^ ((r & 1) << 2);
+    else return ((r >> 1) & 1) | ((((r >> 1) ^ (r >> 2)) & 1) << 1);
+}
+
+// Async copy of one [BK][DP] tile (keys k0.., one kv head) into LDS.  A tile
+// is NI = BK*DP/512 copy instructions of 64 lanes x 16 B (RPI rows each);
+// wavefront w issues instructions w, w + WAVES, ...
+template <typename T, int DP>
+__device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_stride, int keys_valid,
+                                          int D, int wave, int lane) {
+    constexpr int CH = DP / 8;
+    constexpr int RPI = 64 / CH;
+    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int row0 = i * RPI;
+            const int row = row0 + lane / CH;
+            const int chunk = (lane % CH) ^ swz<CH>(row);
+            const void* src = (row < keys_valid && chunk * 8 < D)
+                                   ? static_cast<const void*>(g + row * row_stride + chunk * 8)
+                                   : static_cast<const void*>(g_zero16);
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+        }
+    }
+}
+
+// Byte offset, within a full tile, of the 16-byte chunk lane `lane` copies.
+// The rows a lane copies are wave*RPI + lane/CH plus multiples of WAVES*RPI;
+// when that is a multiple of 16 (full_tile_shortcut), their swizzle (a
+// function of row % 16) is the same for every instruction and one offset
+// serves them all.
+template <int DP> constexpr bool full_tile_shortcut() {
+    return (FaTile<DP>::WAVES * (64 / (DP / 8))) % 16 == 0;
+}
+template <typename T, int DP>
+__device__ __forceinline__ uint32_t full_tile_lane_offset(int64_t row_stride, int wave, int lane) {
+    constexpr int CH = DP / 8;
+    constexpr int RPI = 64 / CH;
+    const int row = wave * RPI + lane / CH;
+    const int chunk = (lane % CH) ^ swz<CH>(row);
+    return (uint32_t)(((int64_t)(lane / CH) * row_stride + chunk * 8) * (int64_t)sizeof(T));
+}
+
+// Async copy of a tile whose 64 rows are all valid and whose rows hold exactly
+// DP elements: a uniform base per instruction plus one per-lane offset.
+template <typename T, int DP>
+__device__ __forceinline__ void load_tile_full(T* tile, const T* g, int64_t row_stride, uint32_t voff,
+                                               int wave) {
+    constexpr int CH = DP / 8;
+    constexpr int RPI = 64 / CH;
+    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
+    static_assert(full_tile_shortcut<DP>(), "one lane offset serves every instruction");
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int row0 = i * RPI;
+            const char* src = reinterpret_cast<const char*>(g + (int64_t)row0 * row_stride) + voff;
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+        }
+    }
+}
+
+// 8 consecutive elements (one 16-byte chunk) of a tile row.
+template <typename T, int DP>
+__device__ __forceinline__ typename V<T>::x8 row_chunk(const T* tile, int row, int chunk) {
+    return *reinterpret_cast<const typename V<T>::x8*>(
+        tile + row * DP + ((chunk ^ swz<DP / 8>(row)) << 3));
+}
+
+// Address of element (row, d) with d % 4 == 0, for the transposing read.
+template <typename T, int DP>
+__device__ __forceinline__ const T* tr_addr(const T* tile, int row, int d) {
+    return tile + row * DP + (((d >> 3) ^ swz<DP / 8>(row)) << 3) + (d & 7);
+}
+
+// A operand V^T[d][k] of the 32-key step kk and 16-wide d block db: lane l
+// (g = l/16) holds d = 16*db + l%16 and keys 32*kk + 4*g + 0..3 (elements
+// 0..3) and 32*kk + 16 + 4*g + 0..3 (elements 4..7).  In ds_read_b64_tr_b16
+// lanes 4q..4q+3 of each 16-lane group address row q's 16 elements; lane j of
+// the group then receives element j of rows 0..3.
+template <typename T, int DP>
+__device__ __forceinline__ typename V<T>::x8 vt_operand(const T* tile, int kk, int db, int lane) {
+    const int g = lane >> 4, j16 = lane & 15;
+    const int row = 32 * kk + 4 * g + (j16 >> 2);
+    const int d = 16 * db + 4 * (j16 & 3);
+    const typename V<T>::x4 lo = lds_read_tr(tr_addr<T, DP>(tile, row, d));
+    const typename V<T>::x4 hi = lds_read_tr(tr_addr<T, DP>(tile, row + 16, d));
+    typename V<T>::x8 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r[j] = lo[j];
+        r[j + 4] = hi[j];
+    }
+    return r;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Packed 16-bit pairs: round-to-nearest-even conversion of two floats and a
+// two-term fp32 dot product with (1, 1), used to sum the rounded values.
+template <typename T> struct Pk;
+template <> struct Pk<bf16> {
+    typedef __bf16 x2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ unsigned cvt(float a, float b) {
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(unsigned, __builtin_convertvector(v, x2));
+    }
+    static __device__ __forceinline__ float sum_into(unsigned pk, float acc) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(x2, pk),
+                                               __builtin_bit_cast(x2, 0x3f803f80u), acc, false);
+    }
+};
+template <> struct Pk<f16> {
+    typedef _Float16 x2 __attribute__((ext_vector_type(2)));
+    static __device__ __forceinline__ unsigned cvt(float a, float b) {
+        const f32x2 v = {a, b};
+        return __builtin_bit_cast(unsigned, __builtin_convertvector(v, x2));
+    }
+    static __device__ __forceinline__ float sum_into(unsigned pk, float acc) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(x2, pk), __builtin_bit_cast(x2, 0x3c003c00u),
+                                      acc, false);
+    }
+};
+
+// Wait until this thread's global->LDS copies have landed (vmcnt = 0); the
+// LDS and scalar counters are left alone.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Reduce x over the four lanes l%16 + 16*g (g = 0..3) that share a query row.
+// v_permlane16_swap / v_permlane32_swap exchange the odd 16-lane (32-lane)
+// groups of their first operand with the even groups of the second; with both
+// operands x, op(r0, r1) combines each lane with its partner in the same
+// operand order in every lane, so all four lanes end with the same value.
+__device__ __forceinline__ float row_sum4(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_max4(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+}  // namespace
+}  // namespace kf

@@ -23,7 +23,9 @@ valid key (bottom-right causal masks with Nq > Nk) give out = 0, tangent = 0
 and LSE = +inf, the FlashAttention convention.
 
 The backward pass (the reference delegates it to flash-attn's
-``_flash_attn_backward``) is not implemented by this build and raises.
+``_flash_attn_backward``, custom.py:252-267) runs on the gfx950 backward
+kernels (``kf_fa_bwd``): dQ per query tile, dK/dV per key tile with the query
+heads of a GQA group summed in a fixed order, so gradients are deterministic.
 """
 
 from __future__ import annotations
@@ -139,6 +141,45 @@ def _fwd_jvp_fake(q, k, v, tq, tk, tv, scale, causal):
     return torch.empty_like(q), lse, torch.empty_like(q)
 
 
+@torch.library.custom_op("kernelforge_amd::flash_attention_bwd", mutates_args=(), device_types="cuda")
+def _bwd_op(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+            lse: torch.Tensor, scale: float, causal: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    B, Nq, Nk, Hq, Hkv, D = _dims(q, k)
+    lib = _lib.load()
+    dq, dk, dv = (torch.empty_like(x, memory_format=torch.contiguous_format) for x in (q, k, v))
+    ws_bytes = lib.kf_fa_bwd_workspace_bytes(B, Nq, Hq, D)
+    if ws_bytes < 0:
+        raise ValueError("flash attention backward: unsupported shape")
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    rc = lib.kf_fa_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(dout),
+                       _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), ws_bytes,
+                       B, Nq, Nk, Hq, Hkv, D, scale, int(causal), _lib.kf_dtype(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "kf_fa_bwd")
+    return dq, dk, dv
+
+
+@_bwd_op.register_fake
+def _bwd_fake(dout, q, k, v, out, lse, scale, causal):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def flash_attention_backward(dout, q, k, v, out, lse, *, softmax_scale=None, causal=False):
+    """``(dq, dk, dv)`` for the output cotangent ``dout`` from the forward's ``out`` and ``lse``.
+
+    The standalone form of ``FlashAttentionFunction.backward`` (the reference
+    calls flash-attn's ``_flash_attn_backward`` there, custom.py:252-267):
+    P is recomputed from the natural-log LSE, no forward is launched.
+    """
+    scale = _validate_inputs(q, k, v, softmax_scale)
+    for name, t in (("dout", dout), ("out", out)):
+        if t.shape != q.shape or t.dtype != q.dtype or t.device != q.device:
+            raise ValueError(f"{name} must have q's shape, device, and dtype")
+    if lse.shape != (q.shape[0], q.shape[2], q.shape[1]) or lse.dtype != torch.float32 or lse.device != q.device:
+        raise ValueError("lse must be float32 [B, Hq, Nq] on q's device")
+    q, k, v, dout, out, lse = (x.contiguous() for x in (q, k, v, dout, out, lse))
+    return _bwd_op(dout, q, k, v, out, lse, scale, bool(causal))
+
+
 # ---------------------------------------------------------------------------
 # Public API.
 # ---------------------------------------------------------------------------
@@ -217,9 +258,13 @@ class FlashAttentionFunction(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, dout, dlse):
-        raise NotImplementedError(
-            "kernelforge_amd: the FlashAttention backward pass is not implemented by this build "
-            "(forward and forward-mode JVP only)")
+        # LSE is non-differentiable: its cotangent is ignored, as in the reference.
+        if dout is None:
+            return (None,) * 5
+        q, k, v, out, lse = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(dout, q, k, v, out, lse, softmax_scale=ctx.softmax_scale,
+                                              causal=ctx.causal)
+        return dq, dk, dv, None, None
 
     @staticmethod
     def jvp(ctx, tq, tk, tv, tscale, tcausal):
@@ -234,7 +279,8 @@ def flash_attention(q, k, v, *, softmax_scale=None, causal=False, return_lse=Fal
 
     Returns out, or (out, lse) with ``return_lse=True``; LSE is a
     non-differentiable natural-log auxiliary output for standalone JVP calls.
-    Supports torch.func.jvp and torch.autograd.forward_ad.  First order only.
+    Supports torch.autograd (backward on the HIP backward kernels), torch.func.jvp
+    and torch.autograd.forward_ad.  First order only.
     """
     _validate_inputs(q, k, v, softmax_scale)
     out, lse = FlashAttentionFunction.apply(q.contiguous(), k.contiguous(), v.contiguous(),

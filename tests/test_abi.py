@@ -38,7 +38,7 @@ def declared_functions():
 
 def test_header_declares_the_abi():
     decls = declared_functions()
-    assert {"kf_rmsnorm_fwd", "kf_linattn_fwd", "kf_fa_fwd", "kf_fa_jvp", "kf_fa_fwd_jvp"} <= set(decls)
+    assert {"kf_rmsnorm_fwd", "kf_linattn_fwd", "kf_fa_fwd", "kf_fa_jvp", "kf_fa_fwd_jvp", "kf_fa_bwd"} <= set(decls)
 
 
 def test_every_declared_symbol_is_exported_and_bound(lib):
@@ -77,6 +77,14 @@ def test_host_side_validation_needs_no_device(lib):
     assert b"scale" in lib.kf_last_error()
     assert lib.kf_fa_jvp(null, null, null, null, null, null, null, null, null,
                          1, 4, 4, 2, 2, 64, 0.1, 0, _lib.KF_F32, null) == 1
+    bwd_args = (null,) * 9
+    assert lib.kf_fa_bwd(*bwd_args, null, 0, 1, 4, 4, 3, 2, 64, 0.1, 0, _lib.KF_BF16, null) == 1
+    assert b"multiple of Hkv" in lib.kf_last_error()
+    assert lib.kf_fa_bwd(*bwd_args, null, 0, 1, 4, 4, 2, 2, 264, 0.1, 0, _lib.KF_BF16, null) == 1
+    # a workspace smaller than kf_fa_bwd_workspace_bytes is refused before any launch
+    need = lib.kf_fa_bwd_workspace_bytes(1, 4, 2, 64)
+    assert lib.kf_fa_bwd(*bwd_args, null, need - 1, 1, 4, 4, 2, 2, 64, 0.1, 0, _lib.KF_BF16, null) == 3
+    assert lib.kf_fa_bwd(*bwd_args, null, 0, 0, 4, 4, 2, 2, 64, 0.1, 0, _lib.KF_BF16, null) == 0
 
 
 def test_workspace_size_formula(lib):
@@ -84,3 +92,8 @@ def test_workspace_size_formula(lib):
     for B, H, D, S in ((2, 70, 32, 15), (1, 1, 8, 1), (3, 4, 128, 7)):
         assert lib.kf_linattn_workspace_bytes(B, H, D, S) >= 4 * B * H * (D + 1) * D * (S + 1)
     assert lib.kf_linattn_workspace_bytes(1, 1, 48, 1) == 0
+    # fp32 [LSE*log2e, Delta] per (batch, head, row), rows padded to the query tile
+    assert lib.kf_fa_bwd_workspace_bytes(2, 1000, 16, 128) == 8 * 2 * 16 * 1024
+    assert lib.kf_fa_bwd_workspace_bytes(1, 65, 3, 256) == 8 * 3 * 128
+    assert lib.kf_fa_bwd_workspace_bytes(1, 0, 3, 64) == 0
+    assert lib.kf_fa_bwd_workspace_bytes(1, 8, 3, 264) == -1

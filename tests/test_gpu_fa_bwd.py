@@ -1,0 +1,164 @@
+"""FlashAttention backward parity on the GPU (HIP kf_fa_bwd via autograd vs the CPU oracle).
+
+The reference gets its gradients from flash-attn's ``_flash_attn_backward``
+(flash_attention_jvp/custom.py:252-267) and checks them in
+flash_attention_jvp/test.py: ``test_autograd_interfaces`` (:124-140, gradients
+of ``flash_attention`` with and without ``return_lse`` against CPU fp64
+autograd of ``attention``) and ``test_finite_difference_and_duality``
+(:186-191, <JVP(t), c> == <t, VJP(c)>).  Both are restated here, and the
+gradient check is widened to the reference's whole shape table (partial
+tiles, padded head dims, GQA/MQA, bottom-right causal masks with empty rows,
+head dims up to 256).  Tolerances are the reference's: bf16 3e-2/3e-2 and fp16
+3e-3/1e-2 against CPU fp64; 2e-2/2e-2 against fp32 torch autograd at the
+BASELINE config shape (B=2, H=16, N=4096, D=128).
+"""
+
+import pytest
+import torch
+
+from kernelforge_amd.flash_attention_jvp import flash_attention, flash_attention_backward, flash_attention_jvp
+from oracle import fa as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DTYPES = (torch.float16, torch.bfloat16)
+# B, Nq, Nk, Hq, Hkv, D, causal, scale: flash_attention_jvp/test.py:25-38 plus
+# the head dims above 128.
+CASES = (
+    (1, 7, 11, 2, 2, 8, False, None),
+    (2, 33, 65, 4, 4, 24, False, 0.3),
+    (1, 129, 131, 3, 3, 64, False, None),
+    (1, 65, 65, 2, 2, 64, True, None),
+    (1, 19, 71, 4, 2, 96, True, None),
+    (1, 71, 19, 4, 1, 32, True, None),
+    (1, 37, 91, 6, 2, 128, False, 0.2),
+    (1, 9, 13, 2, 1, 256, False, None),
+    (1, 1, 1, 2, 2, 64, True, None),
+    (1, 17, 29, 2, 2, 16, False, 0.05),
+    (1, 23, 37, 2, 2, 80, False, 0.15),
+    (1, 999, 515, 2, 2, 64, False, None),
+    (1, 130, 97, 2, 1, 256, True, None),
+    (2, 70, 45, 2, 2, 200, False, 0.1),
+    (1, 64, 256, 1, 1, 136, False, None),
+    (1, 200, 200, 4, 2, 256, False, None),
+    (1, 300, 300, 8, 1, 128, True, None),
+)
+
+
+def tolerance(dtype):
+    return {torch.float16: dict(atol=3e-3, rtol=1e-2), torch.bfloat16: dict(atol=3e-2, rtol=3e-2)}[dtype]
+
+
+def make_inputs(case, dtype, *, noncontiguous=False, seed=2026):
+    """q, k, v and an output cotangent, drawn on the CPU from a seeded generator."""
+    b, nq, nk, h, hk, d, _, _ = case
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for shape in ((b, nq, h, d), (b, nk, hk, d), (b, nk, hk, d), (b, nq, h, d)):
+        if noncontiguous:
+            x = torch.randn((*shape[:-1], shape[-1] * 2), generator=g).to(dtype).to(DEV)[..., ::2]
+        else:
+            x = torch.randn(shape, generator=g).to(dtype).to(DEV)
+        out.append(x)
+    return tuple(out)
+
+
+def hip_grads(q, k, v, cot, **kwargs):
+    prim = tuple(x.detach().clone().requires_grad_() for x in (q, k, v))
+    out = flash_attention(*prim, **kwargs)
+    return torch.autograd.grad(out, prim, cot)
+
+
+def fp64_grads(q, k, v, cot, **kwargs):
+    prim = tuple(x.detach().cpu().double().requires_grad_() for x in (q, k, v))
+    ref = orc.attention(*prim, **kwargs)
+    return torch.autograd.grad(ref, prim, cot.detach().cpu().double())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", CASES)
+def test_gradients_match_fp64(case, dtype):
+    q, k, v, cot = make_inputs(case, dtype)
+    kwargs = dict(causal=case[-2], softmax_scale=case[-1])
+    grads = hip_grads(q, k, v, cot, **kwargs)
+    for name, actual, ref, primal in zip(("dq", "dk", "dv"), grads, fp64_grads(q, k, v, cot, **kwargs), (q, k, v)):
+        assert actual.shape == primal.shape and actual.dtype == dtype, name
+        assert torch.isfinite(actual).all(), name
+        torch.testing.assert_close(actual.cpu().double(), ref, **tolerance(dtype), msg=lambda m: f"{name}: {m}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", (False, True))
+def test_autograd_interfaces_backward(dtype, causal):
+    """flash_attention_jvp/test.py:124-140 on non-contiguous inputs."""
+    case = (1, 67, 41, 4, 2, 64, causal, 0.17)
+    q, k, v, cot = make_inputs(case, dtype, noncontiguous=True)
+    kwargs = dict(causal=causal, softmax_scale=case[-1])
+    prim = tuple(x.detach().requires_grad_() for x in (q, k, v))
+    actual_grads = torch.autograd.grad(flash_attention(*prim, **kwargs), prim, cot)
+    stats_out, lse = flash_attention(*prim, return_lse=True, **kwargs)
+    assert not lse.requires_grad
+    stats_grads = torch.autograd.grad(stats_out, prim, cot)
+    reference = fp64_grads(q, k, v, cot, **kwargs)
+    for actual, stats, ref in zip(actual_grads, stats_grads, reference):
+        # No atomics: the two backward launches give identical bits.
+        torch.testing.assert_close(stats, actual, atol=0, rtol=0)
+        torch.testing.assert_close(actual.cpu().double(), ref, **tolerance(dtype))
+
+
+def test_jvp_vjp_duality():
+    """<JVP(t), c> == sum <t_x, VJP(c)_x> (flash_attention_jvp/test.py:186-191)."""
+    g = torch.Generator().manual_seed(2026)
+    shapes = ((1, 23, 4, 32), (1, 31, 2, 32), (1, 31, 2, 32))
+    q, k, v, tq, tk, tv = (torch.randn(s, generator=g).half().to(DEV) for s in (*shapes, *shapes))
+    out, lse = flash_attention(q, k, v, causal=True, return_lse=True)
+    tangent = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, causal=True)
+    cot = torch.randn(out.shape, generator=g).half().to(DEV)
+    grads = hip_grads(q, k, v, cot, causal=True)
+    lhs = (tangent.float() * cot.float()).sum()
+    rhs = sum((gr.float() * t.float()).sum() for gr, t in zip(grads, (tq, tk, tv)))
+    torch.testing.assert_close(lhs, rhs, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_deterministic_and_standalone(dtype):
+    """Repeated backward passes give identical bits (GQA group of 4 summed in a
+    fixed order), and the standalone entry point matches autograd."""
+    case = (2, 150, 170, 8, 2, 64, False, None)
+    q, k, v, cot = make_inputs(case, dtype)
+    first = hip_grads(q, k, v, cot)
+    second = hip_grads(q, k, v, cot)
+    out, lse = flash_attention(q, k, v, return_lse=True)
+    standalone = flash_attention_backward(cot, q, k, v, out, lse)
+    for a, b, c in zip(first, second, standalone):
+        torch.testing.assert_close(b, a, atol=0, rtol=0)
+        torch.testing.assert_close(c, a, atol=0, rtol=0)
+    with pytest.raises(ValueError, match="lse"):
+        flash_attention_backward(cot, q, k, v, out, lse.half())
+    with pytest.raises(ValueError, match="dout"):
+        flash_attention_backward(cot[:, :-1], q, k, v, out, lse)
+
+
+def test_empty_rows_have_zero_dq():
+    """Bottom-right causal with Nq > Nk: rows i < Nq - Nk see no key (LSE = +inf)
+    and get dq = 0; keys still receive the gradients of the other rows."""
+    case = (1, 71, 19, 4, 1, 32, True, None)
+    q, k, v, cot = make_inputs(case, torch.bfloat16)
+    dq, dk, dv = hip_grads(q, k, v, cot, causal=True)
+    assert torch.count_nonzero(dq[:, : 71 - 19]) == 0
+    assert torch.count_nonzero(dq[:, 71 - 19:]) > 0
+    assert torch.isfinite(dk).all() and torch.isfinite(dv).all()
+
+
+@pytest.mark.parametrize("causal", (False, True))
+def test_baseline_config_backward(causal):
+    """B=2, H=16, N=4096, D=128 bf16 against fp32 torch autograd on the GPU."""
+    B, H, N, D = 2, 16, 4096, 128
+    g = torch.Generator().manual_seed(0)
+    q, k, v, cot = (torch.randn((B, N, H, D), generator=g).to(torch.bfloat16).to(DEV) for _ in range(4))
+    grads = hip_grads(q, k, v, cot, causal=causal)
+    prim = tuple(x.detach().float().requires_grad_() for x in (q, k, v))
+    ref = torch.autograd.grad(orc.attention(*prim, causal=causal), prim, cot.float())
+    for name, actual, r in zip(("dq", "dk", "dv"), grads, ref):
+        torch.testing.assert_close(actual.float(), r, atol=2e-2, rtol=2e-2, msg=lambda m: f"{name}: {m}")
+        assert ((actual.float() - r).norm() / r.norm()).item() < 1e-2
