@@ -334,8 +334,7 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
         if (wave < 2 && (kBR == 64 || lane < kBR)) {
             const float* src = (wave == 0 ? p.ws_lse2 : p.ws_delta) +
                                ((int64_t)b * p.Hq + hq) * p.nq_pad + r0 + lane;
-            __builtin_amdgcn_global_load_lds(
-                src, (__attribute__((address_space(3))) void*)lds_stats(bufc, wave), 4, 0, 0);
+            lds_copy4(src, __builtin_amdgcn_readfirstlane(lds_addr(lds_stats(bufc, wave))));
         }
     };
 

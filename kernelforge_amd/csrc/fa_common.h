@@ -2,6 +2,15 @@
 // fa_jvp.hip, backward in fa_bwd.hip) for gfx950: workgroup shapes, the
 // HBM -> LDS tile copies (global_load_lds), the XOR chunk swizzle and the LDS
 // operand reads for v_mfma_f32_16x16x32, and 16-lane-group row reductions.
+//
+// The HBM -> LDS copies are issued from inline assembly.  The compiler models
+// a global_load_lds it emits itself as a FLAT access of both VMEM and LDS and,
+// while one is outstanding, turns the next wait for any LDS read or global
+// load into vmcnt(0) lgkmcnt(0): the wavefront then stalls until the copy of
+// the NEXT tile has landed, which defeats the double buffering.  Issued from
+// assembly, the copies are invisible to that model; the kernels wait for them
+// explicitly (wait_vmem) before the barrier that publishes a buffer, and the
+// "memory" clobber keeps the compiler from moving LDS accesses across them.
 #pragma once
 
 #include <type_traits>
@@ -12,6 +21,23 @@ namespace kf {
 namespace {
 
 enum FaMode { FA_FWD = 0, FA_FWD_JVP = 1, FA_JVP = 2 };
+
+// Byte address of an LDS location, as the M0 register of an LDS copy takes it.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// HBM -> LDS copy of 16 bytes per lane: lane i's bytes at `src` land at LDS
+// address m0 + 16 i.  m0 must be wavefront-uniform.  The s_nop covers the
+// wait state an LDS copy needs after M0 is written.
+__device__ __forceinline__ void lds_copy16(const void* src, uint32_t m0) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// The same with 4 bytes per lane (lane i's dword lands at m0 + 4 i).
+__device__ __forceinline__ void lds_copy4(const void* src, uint32_t m0) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
 
 // Workgroup shape per padded head dim.  Up to D = 128: 8 wavefronts x 16
 // query rows, 64-key tiles, two wavefronts per SIMD.  D = 256 doubles the Q and
@@ -83,8 +109,7 @@ __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_strid
             const void* src = (row < keys_valid && chunk * 8 < D)
                                    ? static_cast<const void*>(g + row * row_stride + chunk * 8)
                                    : static_cast<const void*>(g_zero16);
-            __builtin_amdgcn_global_load_lds(
-                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + row0 * DP)));
         }
     }
 }
@@ -121,8 +146,7 @@ __device__ __forceinline__ void load_tile_full(T* tile, const T* g, int64_t row_
         if (NI % W == 0 || i < NI) {
             const int row0 = i * RPI;
             const char* src = reinterpret_cast<const char*>(g + (int64_t)row0 * row_stride) + voff;
-            __builtin_amdgcn_global_load_lds(
-                src, (__attribute__((address_space(3))) void*)(tile + row0 * DP), 16, 0, 0);
+            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + row0 * DP)));
         }
     }
 }
@@ -189,8 +213,9 @@ template <> struct Pk<f16> {
     }
 };
 
-// Wait until this thread's global->LDS copies have landed (vmcnt = 0); the
-// LDS and scalar counters are left alone.
+// Wait until this thread's global->LDS copies (and any other vector memory
+// operation) have completed (vmcnt = 0); the LDS and scalar counters are left
+// alone.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Reduce x over the four lanes l%16 + 16*g (g = 0..3) that share a query row.

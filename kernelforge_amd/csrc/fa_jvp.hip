@@ -28,58 +28,85 @@
 // Memory.  K, V (and tK, tV) tiles stream HBM -> LDS with global_load_lds
 // (16 B per lane, no VGPR staging), double buffered, rows XOR-swizzled in
 // 16-byte chunks so that neither the row reads (ds_read_b128) nor the
-// transposing reads (ds_read_b64_tr_b16) conflict in the LDS banks.  Workgroups are renumbered so that all query tiles of one head run
-// on one XCD and share its L2.
+// transposing reads (ds_read_b64_tr_b16) conflict in the LDS banks.
+// Workgroups are renumbered so that all query tiles of one head run on one
+// XCD and share its L2.
+//
+// Operand pipelining.  The LDS reads of the MFMA operands (K rows, V^T
+// columns) run a fixed number of steps ahead of the MFMAs that consume them,
+// in small register rings; sched_barrier fences keep the compiler from
+// sinking the reads back next to their uses, where each LDS latency would be
+// exposed.  The first V^T operands of a half are read before the softmax
+// arithmetic, so they arrive while it runs.
 //
 // Exponent reference.  FWD/FWD_JVP fix each row's reference m at the max of
-// its first key tile and never raise it, so U and G are never rescaled inside
+// its first 32 keys and never raise it, so U and G are never rescaled inside
 // the scan.  A later score exceeding m by ~2^7 (log2 units; 2^4 for fp16 E)
 // overflows to a non-finite accumulator, which the workgroup detects at the
-// end and answers by redoing its rows with a lazily rescaling scan.
+// end and answers by redoing its rows with a lazily rescaling scan (an
+// out-of-line function).  The JVP-from-LSE mode uses -LSE as the reference.
 #include "fa_common.h"
 
 namespace kf {
 namespace {
 
-template <typename T, int DP, int MODE>
-__global__ __launch_bounds__(FaTile<DP>::THREADS)
-__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
-void fa_kernel(const FaParams p) {
-    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK, kWaves = FaTile<DP>::WAVES;
+// Query tile, head and batch of this workgroup.  XCD-aware renumbering: the
+// hardware sends block i to XCD i % 8; give each XCD a contiguous range of
+// logical blocks (consecutive query tiles of a head).
+struct FaBlock {
+    int qtile, hq, b;
+};
+__device__ __forceinline__ FaBlock fa_block(const FaParams& p) {
+    const int nblk = gridDim.x, id = blockIdx.x;
+    const int per = nblk >> 3, rem = nblk & 7, xcd = id & 7, slot = id >> 3;
+    const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    FaBlock r;
+    r.qtile = logical % p.n_qtiles;
+    const int rest = logical / p.n_qtiles;
+    r.hq = rest % p.Hq;
+    r.b = rest / p.Hq;
+    if (p.causal) r.qtile = p.n_qtiles - 1 - r.qtile;  // longest scans first
+    return r;
+}
+
+// One workgroup's rows: the scan over its key tiles and the epilogue.
+// LAZY = false (the fast path): the exponent reference of a row is fixed at
+// the max of its first 32 keys.  A later score far above it overflows the
+// state; the workgroup then writes NaN into the LSE of its rows (and nothing
+// else), and fa_fixup_kernel redoes those rows with LAZY = true, which raises
+// the reference whenever a half's max exceeds it by 2^3 and rescales the
+// state.  kbuf0/1 and vbuf0/1 are the two K-side and V-side LDS buffers, NT
+// tiles each.
+template <typename T, int DP, int MODE, bool ALL, bool LAZY>
+__device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T* vbuf0, T* vbuf1) {
+    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK;
     constexpr bool JVP = MODE != FA_FWD;
     constexpr int NT = JVP ? 2 : 1;   // tensors per side: K (, tK) and V (, tV)
     constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
     constexpr int DB = DP / 16;        // 16-wide d blocks of the outputs
+    constexpr int NSTEP = 2 * DS;      // (key block, K-step) pairs of a half
+    // Operand prefetch distance in MFMA steps; the forward has registers to
+    // spare for a deeper ring.
+    constexpr int PF = JVP ? (DP > 128 ? 1 : 2) : 3;
+    constexpr int NR = PF + 1;
+    // At D = 256 (one wavefront per SIMD, 512 registers) the fences cost the
+    // register allocator more than the ordering gains.
+    constexpr bool kFence = DP <= 128;
     typedef typename V<T>::x8 x8;
-    // Double-buffered K-side (K, tK) and V-side (V, tV) tiles.  Each buffer is
-    // its own LDS variable so that the compiler's alias analysis separates the
-    // copies into one buffer from the reads of the other.
-    __shared__ __attribute__((aligned(16))) T kside0[NT][kBK * DP];
-    __shared__ __attribute__((aligned(16))) T kside1[NT][kBK * DP];
-    __shared__ __attribute__((aligned(16))) T vside0[NT][kBK * DP];
-    __shared__ __attribute__((aligned(16))) T vside1[NT][kBK * DP];
     auto lds_tile = [&](auto bufc, auto vsc, int i) -> T* {
         constexpr int buf = decltype(bufc)::value;
         if constexpr (decltype(vsc)::value)
-            return buf == 0 ? vside0[i] : vside1[i];
+            return (buf == 0 ? vbuf0 : vbuf1) + i * (kBK * DP);
         else
-            return buf == 0 ? kside0[i] : kside1[i];
+            return (buf == 0 ? kbuf0 : kbuf1) + i * (kBK * DP);
     };
-    __shared__ int bail_vote[kWaves];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;  // 16-lane group: key sub-range / d sub-range
 
-    // XCD-aware renumbering: hardware sends block i to XCD i % 8; give each XCD
-    // a contiguous range of logical blocks (consecutive query tiles of a head).
-    const int nblk = gridDim.x, id = blockIdx.x;
-    const int per = nblk >> 3, rem = nblk & 7, xcd = id & 7, slot = id >> 3;
-    const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-    int qtile = logical % p.n_qtiles;
-    const int rest = logical / p.n_qtiles;
-    const int hq = rest % p.Hq, b = rest / p.Hq;
-    if (p.causal) qtile = p.n_qtiles - 1 - qtile;  // longest scans first
+    const FaBlock blk = fa_block(p);
+    const int qtile = blk.qtile, hq = blk.hq, b = blk.b;
     const int hk = hq / p.group;
 
     const int q0w = qtile * kBQ + wave * 16;     // first row of this wavefront
@@ -91,9 +118,11 @@ void fa_kernel(const FaParams p) {
     const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
     const int diag = p.Nk - p.Nq;                // key j valid for row i iff j <= i + diag
 
-    const bool has_tq = JVP && p.tq != nullptr;
-    const bool has_tk = JVP && p.tk != nullptr;
-    const bool has_tv = JVP && p.tv != nullptr;
+    // Tangent presence: ALL instantiations have every tangent; the others
+    // skip the products of the NULL ones.
+    const bool use_tq = JVP && (ALL || p.tq != nullptr);
+    const bool use_tk = JVP && (ALL || p.tk != nullptr);
+    const bool use_tv = JVP && (ALL || p.tv != nullptr);
 
     // Q (and tQ) as B operands: lane l holds row qr, d = 32*ds + 8*grp + 0..7.
     x8 qreg[DS], tqreg[DS];
@@ -105,17 +134,11 @@ void fa_kernel(const FaParams p) {
         const u32x4 a = ok ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.q) + q_off + d) : z;
         qreg[ds] = __builtin_bit_cast(x8, a);
         if constexpr (JVP) {
-            const u32x4 t = (ok && has_tq)
+            const u32x4 t = (ok && use_tq)
                                 ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.tq) + q_off + d)
                                 : z;
             tqreg[ds] = __builtin_bit_cast(x8, t);
         }
-    }
-
-    // JVP mode: -LSE in log2 units is the exponent offset (+inf LSE -> P = 0).
-    float nref_lse = 0.f;
-    if constexpr (MODE == FA_JVP) {
-        nref_lse = row_ok ? -p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : -__builtin_inff();
     }
 
     // Key range of the workgroup.
@@ -129,21 +152,25 @@ void fa_kernel(const FaParams p) {
     // r_run sum the 16-bit E and H values the products consume, so O is an
     // exact convex combination of V rows and tO = sum_j H_j (v_j - O) / l;
     // l_lse sums the fp32 E for the LSE output.  m_run is in log2 units.
-    struct Stats {
-        float m_run, l_run, r_run, l_lse;
-    };
+    float m_run = -__builtin_inff(), l_run = 0.f, r_run = 0.f, l_lse = 0.f;
+    // Exponent offset: -m_run, or -LSE (log2 units) in the JVP mode (+inf LSE
+    // -> P = 0).
+    float nref = 0.f;
+    if constexpr (MODE == FA_JVP) {
+        nref = row_ok ? -p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : -__builtin_inff();
+    }
 
-    // Full tiles (all 64 keys valid, D == DP) take the uniform-address copy.
+    // Full tiles (all keys valid, D == DP) take the uniform-address copy.
     const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane) : 0u;
     const bool dense_rows = p.D == DP;
     const T* const kbase = static_cast<const T*>(p.k) + kv_base;
     const T* const vbase = static_cast<const T*>(p.v) + kv_base;
-    const T* const tkbase = JVP && has_tk ? static_cast<const T*>(p.tk) + kv_base : nullptr;
-    const T* const tvbase = JVP && has_tv ? static_cast<const T*>(p.tv) + kv_base : nullptr;
+    const T* const tkbase = use_tk ? static_cast<const T*>(p.tk) + kv_base : nullptr;
+    const T* const tvbase = use_tv ? static_cast<const T*>(p.tv) + kv_base : nullptr;
     auto tile_masked = [&](int k0) {
         return (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
     };
-    // A tile's 64 keys are consumed in two halves of 32 (key blocks 2h, 2h+1).
+    // A tile's keys are consumed in halves of 32 (key blocks 2h, 2h+1).
     auto apply_mask = [&](f32x4 (&s)[2], int k0, int h) {
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2)
@@ -160,293 +187,306 @@ void fa_kernel(const FaParams p) {
         return row_max4(mx) * c;
     };
 
-    // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
-    auto epilogue = [&](const f32x4 (&u)[DB], const f32x4 (&g)[DB], const Stats& st) {
-        const float l_tot = row_sum4(st.l_run);
-        const float r_tot = row_sum4(st.r_run);
-        const float l_lse_tot = row_sum4(st.l_lse);
-        T* orow = static_cast<T*>(p.o) + q_off;
-        T* torow = static_cast<T*>(p.to) + q_off;
-        const bool empty = !(l_tot > 0.f);
-        const float inv = empty ? 0.f : 1.f / l_tot;
-        const float rl = r_tot * inv;
+    // Copies of one side of tile `tile` into its buffer: the K side (K, tK)
+    // or the V side (V, tV).  The two sides are issued at different points of
+    // the previous tile's work so that the wavefronts of a workgroup do not
+    // all queue their copies at the same moment.  `bufc` and `vsc` are
+    // compile-time constants (std::integral_constant), so each copy names its
+    // destination buffer statically.
+    auto issue_side = [&](int tile, auto bufc, auto vsc) {
+        constexpr bool vs = decltype(vsc)::value;
+        const int k0 = tile * kBK;
+        const int64_t off = (int64_t)k0 * kv_row_stride;
+        T* const d0 = lds_tile(bufc, vsc, 0);
+        T* const d1 = lds_tile(bufc, vsc, NT - 1);
+        const T* const s0 = (vs ? vbase : kbase) + off;
+        const T* const s1 = (vs ? tvbase : tkbase) + off;
+        const bool tan = JVP && (vs ? use_tv : use_tk);
+        if constexpr (full_tile_shortcut<DP>()) {
+            if (dense_rows && k0 + kBK <= p.Nk) {
+                load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
+                if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
+                return;
+            }
+        }
+        const int kv = p.Nk - k0;
+        load_tile<T, DP>(d0, s0, kv_row_stride, kv, p.D, wave, lane);
+        if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
+    };
+
+    // Operand rings: slot st % NR holds the operands of MFMA step st.
+    x8 kring[NR], tkring[NR], vring[NR], tvring[NR];
+    auto k_load = [&](auto bufc, int h, int st) {
+        const int i2 = st / DS, ds = st % DS;
+        const int krow = 16 * (2 * h + i2) + (lane & 15);
+        kring[st % NR] = row_chunk<T, DP>(lds_tile(bufc, std::false_type{}, 0), krow, 4 * ds + grp);
+        if constexpr (JVP) {
+            if (use_tk)
+                tkring[st % NR] = row_chunk<T, DP>(lds_tile(bufc, std::false_type{}, NT - 1), krow, 4 * ds + grp);
+        }
+    };
+    auto v_load = [&](auto bufc, int h, int db) {
+        vring[db % NR] = vt_operand<T, DP>(lds_tile(bufc, std::true_type{}, 0), h, db, lane);
+        if constexpr (JVP) {
+            if (use_tv) tvring[db % NR] = vt_operand<T, DP>(lds_tile(bufc, std::true_type{}, NT - 1), h, db, lane);
+        }
+    };
+
+    // S^T (and tS^T) of key blocks 2h, 2h+1 of the tile in buffer bufc; ends
+    // by reading the first V^T operands of the same half.
+    auto scores = [&](auto bufc, int h, f32x4 (&s)[2], f32x4 (&ts)[2]) {
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+            s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+            ts[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int st = 0; st < PF && st < NSTEP; ++st) k_load(bufc, h, st);
+#pragma unroll
+        for (int st = 0; st < NSTEP; ++st) {
+            if (st + PF < NSTEP) k_load(bufc, h, st + PF);
+            if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            const int i2 = st / DS, ds = st % DS;
+            const x8 ka = kring[st % NR];
+            s[i2] = mfma16x16x32(ka, qreg[ds], s[i2]);
+            if constexpr (JVP) {
+                if (use_tq) ts[i2] = mfma16x16x32(ka, tqreg[ds], ts[i2]);
+                if (use_tk) ts[i2] = mfma16x16x32(tkring[st % NR], qreg[ds], ts[i2]);
+            }
+            if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int db = 0; db < PF && db < DB; ++db) v_load(bufc, h, db);
+    };
+
+    // E = exp2(S*c + nref) and H = E * scale * tS, packed to 16 bits; their
+    // rounded values are summed into l and r.
+    auto probs = [&](const f32x4 (&s)[2], const f32x4 (&ts)[2], u32x2 (&ew)[2], u32x2 (&hw)[2]) {
+        float esum = 0.f;
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref));
+                const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref));
+                if constexpr (MODE != FA_JVP) esum += e0 + e1;
+                const unsigned pe = Pk<T>::cvt(e0, e1);
+                ew[i2][j] = pe;
+                l_run = Pk<T>::sum_into(pe, l_run);
+                if constexpr (JVP) {
+                    const unsigned ph = Pk<T>::cvt(e0 * (ts[i2][2 * j] * p.scale), e1 * (ts[i2][2 * j + 1] * p.scale));
+                    hw[i2][j] = ph;
+                    r_run = Pk<T>::sum_into(ph, r_run);
+                }
+            }
+        if constexpr (MODE != FA_JVP) l_lse += esum;
+    };
+
+    f32x4 u[DB], g[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        u[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        g[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the 32 keys of half h
+    // of the tile in buffer bufc.
+    auto pv = [&](auto bufc, int h, const u32x2 (&ew)[2], const u32x2 (&hw)[2]) {
+        const x8 eb = __builtin_bit_cast(x8, u32x4{ew[0][0], ew[0][1], ew[1][0], ew[1][1]});
+        const x8 hb = __builtin_bit_cast(x8, u32x4{hw[0][0], hw[0][1], hw[1][0], hw[1][1]});
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-            const int d = 16 * db + 4 * grp;
-            if (row_ok && d < p.D) {
-                typename V<T>::x4 ov, tv;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float o = u[db][e] * inv;
-                    ov[e] = (T)o;
-                    if constexpr (JVP) tv[e] = (T)(g[db][e] * inv - rl * o);
-                }
-                if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
-                if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
+            if (db + PF < DB) v_load(bufc, h, db + PF);
+            if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            const x8 va = vring[db % NR];
+            u[db] = mfma16x16x32(va, eb, u[db]);
+            if constexpr (JVP) {
+                g[db] = mfma16x16x32(va, hb, g[db]);
+                if (use_tv) g[db] = mfma16x16x32(tvring[db % NR], eb, g[db]);
             }
-        }
-        if (MODE != FA_JVP && grp == 0 && row_ok) {
-            p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] =
-                empty ? __builtin_inff() : (st.m_run + log2f(l_lse_tot)) * kLn2;
+            if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
-    // The scan is instantiated twice: branch-free when every tangent is
-    // present (the common case), and with per-tangent checks otherwise.
-    auto scan = [&](auto all_tag) {
-        constexpr bool ALL = decltype(all_tag)::value;
-        const bool use_tq = ALL || has_tq, use_tk = ALL || has_tk, use_tv = ALL || has_tv;
-
-        // Copies of one side of tile `tile` into its buffer: the K side (K,
-        // tK) or the V side (V, tV).  The two halves are issued at different
-        // points of the previous tile's work so that the wavefronts of a
-        // workgroup do not all queue their copies at the same moment.
-        // `bufc` and `vsc` are compile-time constants (std::integral_constant):
-        // with the destination buffer known statically, the compiler can tell
-        // these LDS writes apart from reads of the other buffer and does not
-        // make those reads wait for the copies in flight.
-        auto issue_side = [&](int tile, auto bufc, auto vsc) {
-            constexpr int buf = decltype(bufc)::value;
-            constexpr bool vs = decltype(vsc)::value;
-            const int k0 = tile * kBK;
-            const int64_t off = (int64_t)k0 * kv_row_stride;
-            T* const d0 = lds_tile(bufc, vsc, 0);
-            T* const d1 = lds_tile(bufc, vsc, NT - 1);
-            const T* const s0 = (vs ? vbase : kbase) + off;
-            const T* const s1 = (vs ? tvbase : tkbase) + off;
-            const bool tan = JVP && (vs ? use_tv : use_tk);
-            if constexpr (full_tile_shortcut<DP>()) {
-                if (dense_rows && k0 + kBK <= p.Nk) {
-                    load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
-                    if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
-                    return;
+    // LAZY: raise the reference of rows whose max grew past m + 2^3 and
+    // rescale their state (alpha = 0 for a row leaving m = -inf, whose state
+    // is zero).
+    auto rebase = [&](const f32x4 (&s)[2]) {
+        const float mx = row_max(s);
+        const bool upd = mx > m_run + kRescaleThreshold;
+        if (__any(upd)) {
+            const float alpha = upd ? fast_exp2(m_run - mx) : 1.f;
+            if (upd) m_run = mx;
+            l_run *= alpha;
+            r_run *= alpha;
+            l_lse *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    u[db][i] *= alpha;
+                    if constexpr (JVP) g[db][i] *= alpha;
                 }
-            }
-            const int kv = p.Nk - k0;
-            load_tile<T, DP>(d0, s0, kv_row_stride, kv, p.D, wave, lane);
-            if (tan) load_tile<T, DP>(d1, s1, kv_row_stride, kv, p.D, wave, lane);
-        };
-        auto issue = [&](int tile, auto bufc) {
-            issue_side(tile, bufc, std::false_type{});
-            issue_side(tile, bufc, std::true_type{});
-        };
+            nref = m_run == -__builtin_inff() ? 0.f : -m_run;
+        }
+    };
 
-        // S^T (and tS^T) of key blocks 2h, 2h+1 of the tile in buffer bufc.
-        auto scores = [&](auto bufc, int h, f32x4 (&s)[2], f32x4 (&ts)[2]) {
-            const T* Kt = lds_tile(bufc, std::false_type{}, 0);
-            const T* tKt = lds_tile(bufc, std::false_type{}, NT - 1);
-            const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    // One key tile; tile t lives in buffer t & 1 == decltype(bufc)::value.
+    auto step = [&](int t, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const std::integral_constant<int, buf ^ 1> nbuf;
+        const int k0 = t * kBK;
+        const bool masked = tile_masked(k0);
+        wait_vmem();
+        __syncthreads();  // tile t resident; every wavefront is done with tile t-1
+        if (t + 1 < ntiles) issue_side(t + 1, nbuf, std::false_type{});
 #pragma unroll
-            for (int i2 = 0; i2 < 2; ++i2) {
-                s[i2] = zero;
-                ts[i2] = zero;
-                const int krow = 16 * (2 * h + i2) + (lane & 15);
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    const x8 ka = row_chunk<T, DP>(Kt, krow, 4 * ds + grp);
-                    s[i2] = mfma16x16x32(ka, qreg[ds], s[i2]);
-                    if constexpr (JVP) {
-                        if (use_tq) ts[i2] = mfma16x16x32(ka, tqreg[ds], ts[i2]);
-                        if (use_tk) {
-                            const x8 tka = row_chunk<T, DP>(tKt, krow, 4 * ds + grp);
-                            ts[i2] = mfma16x16x32(tka, qreg[ds], ts[i2]);
-                        }
-                    }
-                }
-            }
-        };
-
-        // E = exp2(S*c + nref) (or P for the JVP mode) and H = E * scale * tS,
-        // packed to 16 bits; their rounded values are summed into l and r.
-        auto probs = [&](const f32x4 (&s)[2], const f32x4 (&ts)[2], float nref, u32x2 (&ew)[2],
-                         u32x2 (&hw)[2], Stats& st) {
-            float esum = 0.f;
-#pragma unroll
-            for (int i2 = 0; i2 < 2; ++i2)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref));
-                    const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref));
-                    if constexpr (MODE != FA_JVP) esum += e0 + e1;
-                    const unsigned pe = Pk<T>::cvt(e0, e1);
-                    ew[i2][j] = pe;
-                    st.l_run = Pk<T>::sum_into(pe, st.l_run);
-                    if constexpr (JVP) {
-                        const unsigned ph = Pk<T>::cvt(e0 * (ts[i2][2 * j] * p.scale),
-                                                       e1 * (ts[i2][2 * j + 1] * p.scale));
-                        hw[i2][j] = ph;
-                        st.r_run = Pk<T>::sum_into(ph, st.r_run);
-                    }
-                }
-            if constexpr (MODE != FA_JVP) st.l_lse += esum;
-        };
-
-        // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the 32 keys of half h
-        // of the tile in buffer bufc.
-        auto pv = [&](f32x4 (&u)[DB], f32x4 (&g)[DB], auto bufc, int h, const u32x2 (&ew)[2],
-                      const u32x2 (&hw)[2]) {
-            const T* Vt = lds_tile(bufc, std::true_type{}, 0);
-            const T* tVt = lds_tile(bufc, std::true_type{}, NT - 1);
-            const x8 eb = __builtin_bit_cast(x8, u32x4{ew[0][0], ew[0][1], ew[1][0], ew[1][1]});
-            const x8 hb = __builtin_bit_cast(x8, u32x4{hw[0][0], hw[0][1], hw[1][0], hw[1][1]});
-#pragma unroll
-            for (int db = 0; db < DB; ++db) {
-                const x8 va = vt_operand<T, DP>(Vt, h, db, lane);
-                u[db] = mfma16x16x32(va, eb, u[db]);
-                if constexpr (JVP) {
-                    g[db] = mfma16x16x32(va, hb, g[db]);
-                    if (use_tv) {
-                        const x8 tva = vt_operand<T, DP>(tVt, h, db, lane);
-                        g[db] = mfma16x16x32(tva, eb, g[db]);
-                    }
-                }
-            }
-        };
-
-        auto zero_acc = [&](f32x4 (&acc)[DB]) {
-#pragma unroll
-            for (int db = 0; db < DB; ++db) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        };
-
-        // ---------------- fast scan: fixed exponent reference ----------------
-        {
-            f32x4 u[DB], g[DB];
-            zero_acc(u);
-            zero_acc(g);
-            Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
-            float nref = nref_lse;
+        for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
             f32x4 s[2], ts[2];
             u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
-            // One key tile; tile t lives in buffer t & 1 == decltype(bufc)::value.
-            auto step = [&](int t, auto bufc) {
-                constexpr int buf = decltype(bufc)::value;
-                const std::integral_constant<int, buf ^ 1> nbuf;
-                const int k0 = t * kBK;
-                const bool masked = tile_masked(k0);
-                wait_vmem();
-                __syncthreads();  // tile t resident; every wavefront is done with tile t-1
-                if (t + 1 < ntiles) issue_side(t + 1, nbuf, std::false_type{});
-#pragma unroll
-                for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
-                    scores(bufc, h, s, ts);
-                    if (h == 0 && t + 1 < ntiles) issue_side(t + 1, nbuf, std::true_type{});
-                    if (masked) apply_mask(s, k0, h);
-                    if constexpr (MODE != FA_JVP) {
-                        if (t == 0 && h == 0) {
-                            // Every non-empty row has a valid key among the
-                            // first 32 (masks only cut keys off at the end).
-                            st.m_run = row_max(s);
-                            nref = st.m_run == -__builtin_inff() ? 0.f : -st.m_run;
-                        }
-                    }
-                    probs(s, ts, nref, ew, hw, st);
-                    pv(u, g, bufc, h, ew, hw);
+            scores(bufc, h, s, ts);
+            if (h == 0 && t + 1 < ntiles) issue_side(t + 1, nbuf, std::true_type{});
+            if (masked) apply_mask(s, k0, h);
+            if constexpr (MODE != FA_JVP) {
+                if constexpr (LAZY) {
+                    rebase(s);
+                } else if (t == 0 && h == 0) {
+                    // Every non-empty row has a valid key among its first 32
+                    // (masks only cut keys off at the end).
+                    m_run = row_max(s);
+                    nref = m_run == -__builtin_inff() ? 0.f : -m_run;
                 }
-            };
-            if (ntiles > 0) issue(0, std::integral_constant<int, 0>{});
-            for (int t = 0; t < ntiles; t += 2) {
-                step(t, std::integral_constant<int, 0>{});
-                if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
             }
-            if constexpr (MODE == FA_JVP) {
-                epilogue(u, g, st);
-                return;
-            } else {
-                // Overflow check, made uniform over the workgroup (the
-                // rescaling scan needs every wavefront for its tile copies).
-                bool fin = __builtin_isfinite(st.l_lse) && __builtin_isfinite(st.r_run);
-#pragma unroll
-                for (int db = 0; db < DB; ++db)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        fin = fin && __builtin_isfinite(u[db][i]);
-                        if constexpr (JVP) fin = fin && __builtin_isfinite(g[db][i]);
-                    }
-                const bool wave_bad = __any(!fin);
-                if (lane == 0) bail_vote[wave] = wave_bad;
-                __syncthreads();
-                int any_bad = 0;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) any_bad |= bail_vote[w];
-                if (!any_bad) {
-                    epilogue(u, g, st);
-                    return;
-                }
-                wait_vmem();
-                __syncthreads();
-            }
-        }
-
-        // ---------------- rescaling scan (rare): one tile at a time ----------------
-        if constexpr (MODE != FA_JVP) {
-            f32x4 u[DB], g[DB];
-            zero_acc(u);
-            zero_acc(g);
-            Stats st{-__builtin_inff(), 0.f, 0.f, 0.f};
-            // Copy, wait and consume one tile at a time, always in buffer 0.
-            const std::integral_constant<int, 0> buf0;
-            for (int t = 0; t < ntiles; ++t) {
-                const int k0 = t * kBK;
-                issue(t, buf0);
-                wait_vmem();
-                __syncthreads();
-#pragma unroll
-                for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
-                    f32x4 s[2], ts[2];
-                    u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
-                    scores(buf0, h, s, ts);
-                    if (tile_masked(k0)) apply_mask(s, k0, h);
-                    // Raise the reference only when the max grew by more than
-                    // 2^8: E stays <= 256.  A row leaving m = -inf gets alpha =
-                    // exp2(-inf) = 0 on its all-zero state.
-                    const float mx = row_max(s);
-                    const bool upd = mx > st.m_run + kRescaleThreshold;
-                    const float alpha = upd ? fast_exp2(st.m_run - mx) : 1.f;
-                    if (upd) {
-                        st.m_run = mx;
-                        st.l_run *= alpha;
-                        st.r_run *= alpha;
-                        st.l_lse *= alpha;
-                    }
-                    if (__any(upd)) {
-#pragma unroll
-                        for (int db = 0; db < DB; ++db)
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                u[db][i] *= alpha;
-                                g[db][i] *= alpha;
-                            }
-                    }
-                    probs(s, ts, st.m_run == -__builtin_inff() ? 0.f : -st.m_run, ew, hw, st);
-                    pv(u, g, buf0, h, ew, hw);
-                }
-                __syncthreads();
-            }
-            epilogue(u, g, st);
+            probs(s, ts, ew, hw);
+            pv(bufc, h, ew, hw);
         }
     };
-    if (!JVP || (has_tq && has_tk && has_tv))
-        scan(std::true_type{});
-    else
-        scan(std::false_type{});
+    if (ntiles > 0) {
+        issue_side(0, std::integral_constant<int, 0>{}, std::false_type{});
+        issue_side(0, std::integral_constant<int, 0>{}, std::true_type{});
+    }
+    for (int t = 0; t < ntiles; t += 2) {
+        step(t, std::integral_constant<int, 0>{});
+        if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+    }
+
+    if constexpr (MODE != FA_JVP && !LAZY) {
+        // Overflow check, made uniform over the workgroup (the rescaling scan
+        // needs every wavefront for its tile copies).
+        bool fin = __builtin_isfinite(l_lse) && __builtin_isfinite(r_run);
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                fin = fin && __builtin_isfinite(u[db][i]);
+                if constexpr (JVP) fin = fin && __builtin_isfinite(g[db][i]);
+            }
+        if (__syncthreads_or(!fin)) {
+            if (grp == 0 && row_ok) p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] = __builtin_nanf("");
+            return;
+        }
+    }
+
+    // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
+    const float l_tot = row_sum4(l_run);
+    const float r_tot = row_sum4(r_run);
+    const float l_lse_tot = row_sum4(l_lse);
+    T* orow = static_cast<T*>(p.o) + q_off;
+    T* torow = static_cast<T*>(p.to) + q_off;
+    const bool empty = !(l_tot > 0.f);
+    const float inv = empty ? 0.f : 1.f / l_tot;
+    const float rl = r_tot * inv;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+        const int d = 16 * db + 4 * grp;
+        if (row_ok && d < p.D) {
+            typename V<T>::x4 ov, tv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float o = u[db][e] * inv;
+                ov[e] = (T)o;
+                if constexpr (JVP) tv[e] = (T)(g[db][e] * inv - rl * o);
+            }
+            if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
+            if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
+        }
+    }
+    if (MODE != FA_JVP && grp == 0 && row_ok) {
+        p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] = empty ? __builtin_inff() : (m_run + log2f(l_lse_tot)) * kLn2;
+    }
 }
 
-template <typename T, int MODE>
-int launch_mode(const FaParams& p, int dp, hipStream_t stream) {
+// Double-buffered K-side (K, tK) and V-side (V, tV) tiles.  Each buffer is its
+// own LDS variable so that the compiler's alias analysis separates the copies
+// into one buffer from the reads of the other.
+#define FA_LDS_BUFFERS(T, DP, MODE)                                         \
+    constexpr int NT_ = (MODE) != FA_FWD ? 2 : 1;                          \
+    constexpr int TILE_ = FaTile<DP>::BK * (DP);                           \
+    __shared__ __attribute__((aligned(16))) T kside0[NT_ * TILE_];         \
+    __shared__ __attribute__((aligned(16))) T kside1[NT_ * TILE_];         \
+    __shared__ __attribute__((aligned(16))) T vside0[NT_ * TILE_];         \
+    __shared__ __attribute__((aligned(16))) T vside1[NT_ * TILE_]
+
+template <typename T, int DP, int MODE, bool ALL>
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
+void fa_kernel(const FaParams p) {
+    FA_LDS_BUFFERS(T, DP, MODE);
+    fa_scan<T, DP, MODE, ALL, false>(p, kside0, kside1, vside0, vside1);
+}
+
+// Second launch of the FWD/FWD_JVP modes: a workgroup whose rows carry the
+// overflow marker (NaN LSE) redoes them with the rescaling scan; every other
+// workgroup reads its LSE entries and exits.  A separate kernel keeps the
+// rescaling code out of the fast scan's register allocation.
+template <typename T, int DP, int MODE, bool ALL>
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
+void fa_fixup_kernel(const FaParams p) {
+    const FaBlock blk = fa_block(p);
+    const int row = blk.qtile * FaTile<DP>::BQ + (int)threadIdx.x;
+    bool marked = false;
+    if (threadIdx.x < FaTile<DP>::BQ && row < p.Nq)
+        marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
+    if (!__syncthreads_or(marked)) return;
+    FA_LDS_BUFFERS(T, DP, MODE);
+    fa_scan<T, DP, MODE, ALL, true>(p, kside0, kside1, vside0, vside1);
+}
+
+template <typename T, int MODE, bool ALL>
+int launch_variant(const FaParams& p, int dp, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_qtiles * p.Hq * p.B;
     if (blocks > 0x7fffffff) {
         set_error("fa: grid too large");
         return KF_E_UNSUPPORTED;
     }
     const dim3 grid((unsigned)blocks);
+    auto launch = [&](auto dpc) {
+        constexpr int DP = decltype(dpc)::value;
+        hipLaunchKernelGGL((fa_kernel<T, DP, MODE, ALL>), grid, dim3(FaTile<DP>::THREADS), 0, stream, p);
+        if constexpr (MODE != FA_JVP) {
+            const int rc = check_launch("fa_kernel launch");
+            if (rc != KF_OK) return rc;
+            hipLaunchKernelGGL((fa_fixup_kernel<T, DP, MODE, ALL>), grid, dim3(FaTile<DP>::THREADS), 0, stream, p);
+            return check_launch("fa_fixup_kernel launch");
+        }
+        return check_launch("fa_kernel launch");
+    };
     switch (dp) {
-        case 32: hipLaunchKernelGGL((fa_kernel<T, 32, MODE>), grid, dim3(FaTile<32>::THREADS), 0, stream, p); break;
-        case 64: hipLaunchKernelGGL((fa_kernel<T, 64, MODE>), grid, dim3(FaTile<64>::THREADS), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL((fa_kernel<T, 128, MODE>), grid, dim3(FaTile<128>::THREADS), 0, stream, p); break;
-        case 256: hipLaunchKernelGGL((fa_kernel<T, 256, MODE>), grid, dim3(FaTile<256>::THREADS), 0, stream, p); break;
+        case 32: return launch(std::integral_constant<int, 32>{});
+        case 64: return launch(std::integral_constant<int, 64>{});
+        case 128: return launch(std::integral_constant<int, 128>{});
+        case 256: return launch(std::integral_constant<int, 256>{});
         default: set_error("fa: head dim %d not supported by this build", p.D); return KF_E_UNSUPPORTED;
     }
-    return check_launch("fa_kernel launch");
+}
+
+// The JVP modes have a branch-free instantiation for the common case of
+// three tangents and one that skips the products of NULL tangents.
+template <typename T, int MODE>
+int launch_mode(const FaParams& p, int dp, hipStream_t stream) {
+    if (MODE == FA_FWD || (p.tq && p.tk && p.tv)) return launch_variant<T, MODE, true>(p, dp, stream);
+    return launch_variant<T, MODE, false>(p, dp, stream);
 }
 
 int fa_dispatch(int mode, FaParams p, int dtype, hipStream_t stream) {
