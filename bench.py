@@ -299,7 +299,7 @@ def main() -> int:
             results[name]["speedup_vs_cpu"] = head["gbs"] / cpu["rmsnorm"]["value"]
         if cpu and name.startswith("sana"):
             results[name]["speedup_vs_cpu_sanaA_oracle"] = results[name]["tflops"] / cpu["sana"]["value"]
-        if cpu and name.startswith("fa_"):
+        if cpu and name.startswith("fa_") and name != "fa_bwd":
             results[name]["speedup_vs_cpu"] = results[name]["tflops"] / cpu["fa"]["value"]
         t = traffic.get(results[name]["kernel"] + ":" + results[name]["workload"])
         if t is not None:
