@@ -161,6 +161,11 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
     f32x4 dq[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) dq[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Operand rings (slot st % NR holds step st), as in the forward kernel;
+    // the fences are left out at D = 256, whose register budget is tighter.
+    constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
+    constexpr bool kFence = DP <= 128;
+    x8 kring[NR], vring[NR];
 
     auto step = [&](int t, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
@@ -178,17 +183,33 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
 #pragma unroll
         for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
             f32x4 s[2], dp[2];
+            // K and V rows for step st = (key block i2, K-step ds), read PF
+            // steps ahead of their MFMAs.
+            auto kv_load = [&](int st) {
+                const int krow = 16 * (2 * h + st / DS) + (lane & 15);
+                kring[st % NR] = row_chunk<T, DP>(Kt, krow, 4 * (st % DS) + grp);
+                vring[st % NR] = row_chunk<T, DP>(Vt, krow, 4 * (st % DS) + grp);
+            };
 #pragma unroll
             for (int i2 = 0; i2 < 2; ++i2) {
                 s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
                 dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int krow = 16 * (2 * h + i2) + (lane & 15);
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    s[i2] = mfma16x16x32(row_chunk<T, DP>(Kt, krow, 4 * ds + grp), qreg[ds], s[i2]);
-                    dp[i2] = mfma16x16x32(row_chunk<T, DP>(Vt, krow, 4 * ds + grp), doreg[ds], dp[i2]);
-                }
             }
+#pragma unroll
+            for (int st = 0; st < PF && st < NSTEP; ++st) kv_load(st);
+#pragma unroll
+            for (int st = 0; st < NSTEP; ++st) {
+                if (st + PF < NSTEP) kv_load(st + PF);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                const int i2 = st / DS, ds = st % DS;
+                s[i2] = mfma16x16x32(kring[st % NR], qreg[ds], s[i2]);
+                dp[i2] = mfma16x16x32(vring[st % NR], doreg[ds], dp[i2]);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            }
+            // First K^T operands of the dQ product, in flight during the
+            // softmax arithmetic.
+#pragma unroll
+            for (int db = 0; db < PF && db < DB; ++db) kring[db % NR] = vt_operand<T, DP>(Kt, h, db, lane);
             if (masked) {
 #pragma unroll
                 for (int i2 = 0; i2 < 2; ++i2)
@@ -209,7 +230,12 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
                 }
             const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
 #pragma unroll
-            for (int db = 0; db < DB; ++db) dq[db] = mfma16x16x32(vt_operand<T, DP>(Kt, h, db, lane), sb, dq[db]);
+            for (int db = 0; db < DB; ++db) {
+                if (db + PF < DB) kring[(db + PF) % NR] = vt_operand<T, DP>(Kt, h, db + PF, lane);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                dq[db] = mfma16x16x32(kring[db % NR], sb, dq[db]);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     if (ntiles > 0) {
@@ -344,6 +370,10 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
         dk[db] = f32x4{0.f, 0.f, 0.f, 0.f};
         dv[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // Operand rings, as in the dq kernel.
+    constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
+    constexpr bool kFence = DP <= 128;
+    x8 qring[NR], oring[NR];
 
     auto step = [&](int u, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
@@ -362,17 +392,34 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
         for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
             // S and dP for rows 16*(2h+i2) + 4*grp + i of the tile, key kr.
             f32x4 s[2], dp[2];
+            auto qo_load = [&](int st) {
+                const int row = 16 * (2 * h + st / DS) + (lane & 15);
+                qring[st % NR] = row_chunk<T, DP>(Qt, row, 4 * (st % DS) + grp);
+                oring[st % NR] = row_chunk<T, DP>(Ot, row, 4 * (st % DS) + grp);
+            };
 #pragma unroll
             for (int i2 = 0; i2 < 2; ++i2) {
                 s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
                 dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const int row = 16 * (2 * h + i2) + (lane & 15);
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    s[i2] = mfma16x16x32(row_chunk<T, DP>(Qt, row, 4 * ds + grp), kreg[ds], s[i2]);
-                    dp[i2] = mfma16x16x32(row_chunk<T, DP>(Ot, row, 4 * ds + grp), vreg[ds], dp[i2]);
-                }
             }
+#pragma unroll
+            for (int st = 0; st < PF && st < NSTEP; ++st) qo_load(st);
+#pragma unroll
+            for (int st = 0; st < NSTEP; ++st) {
+                if (st + PF < NSTEP) qo_load(st + PF);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                const int i2 = st / DS, ds = st % DS;
+                s[i2] = mfma16x16x32(qring[st % NR], kreg[ds], s[i2]);
+                dp[i2] = mfma16x16x32(oring[st % NR], vreg[ds], dp[i2]);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            }
+            // First dO^T and Q^T operands of the dV / dK products.
+            auto t_load = [&](int db) {
+                oring[db % NR] = vt_operand<T, DP>(Ot, h, db, lane);
+                qring[db % NR] = vt_operand<T, DP>(Qt, h, db, lane);
+            };
+#pragma unroll
+            for (int db = 0; db < PF && db < DB; ++db) t_load(db);
             u32x2 pw[2], sw[2];
 #pragma unroll
             for (int i2 = 0; i2 < 2; ++i2) {
@@ -396,8 +443,11 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
             const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                dv[db] = mfma16x16x32(vt_operand<T, DP>(Ot, h, db, lane), pb, dv[db]);
-                dk[db] = mfma16x16x32(vt_operand<T, DP>(Qt, h, db, lane), sb, dk[db]);
+                if (db + PF < DB) t_load(db + PF);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                dv[db] = mfma16x16x32(oring[db % NR], pb, dv[db]);
+                dk[db] = mfma16x16x32(qring[db % NR], sb, dk[db]);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
