@@ -69,6 +69,12 @@ __device__ __forceinline__ FaBlock fa_block(const FaParams& p) {
     return r;
 }
 
+// Row blocks of 16 query rows per wavefront.  The forward has the registers
+// for two (a 256-row workgroup): every K row and V^T operand read from LDS
+// then feeds two MFMAs, and a tile copy serves twice the rows.
+template <int DP, int MODE> constexpr int fa_row_blocks() { return MODE == FA_FWD && DP <= 128 ? 2 : 1; }
+template <int DP, int MODE> constexpr int fa_rows() { return FaTile<DP>::BQ * fa_row_blocks<DP, MODE>(); }
+
 // One workgroup's rows: the scan over its key tiles and the epilogue.
 // LAZY = false (the fast path): the exponent reference of a row is fixed at
 // the max of its first 32 keys.  A later score far above it overflows the
@@ -79,7 +85,8 @@ __device__ __forceinline__ FaBlock fa_block(const FaParams& p) {
 // tiles each.
 template <typename T, int DP, int MODE, bool ALL, bool LAZY>
 __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T* vbuf0, T* vbuf1) {
-    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK;
+    constexpr int R = fa_row_blocks<DP, MODE>();
+    constexpr int kBQ = fa_rows<DP, MODE>(), kBK = FaTile<DP>::BK;
     constexpr bool JVP = MODE != FA_FWD;
     constexpr int NT = JVP ? 2 : 1;   // tensors per side: K (, tK) and V (, tV)
     constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
@@ -87,7 +94,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     constexpr int NSTEP = 2 * DS;      // (key block, K-step) pairs of a half
     // Operand prefetch distance in MFMA steps; the forward has registers to
     // spare for a deeper ring.
-    constexpr int PF = JVP ? (DP > 128 ? 1 : 2) : 3;
+    constexpr int PF = JVP ? (DP > 128 ? 0 : 2) : 3;
     constexpr int NR = PF + 1;
     // At D = 256 (one wavefront per SIMD, 512 registers) the fences cost the
     // register allocator more than the ordering gains.
@@ -109,14 +116,21 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     const int qtile = blk.qtile, hq = blk.hq, b = blk.b;
     const int hk = hq / p.group;
 
-    const int q0w = qtile * kBQ + wave * 16;     // first row of this wavefront
-    const int qr = q0w + (lane & 15);            // this lane's query row
-    const bool row_ok = qr < p.Nq;
+    const int q0w = qtile * kBQ + wave * 16 * R;  // first row of this wavefront
     const int64_t q_row_stride = (int64_t)p.Hq * p.D;
     const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
-    const int64_t q_off = ((int64_t)b * p.Nq + qr) * q_row_stride + (int64_t)hq * p.D;
     const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
     const int diag = p.Nk - p.Nq;                // key j valid for row i iff j <= i + diag
+    // This lane's query row in row block rb.
+    int qr[R];
+    bool row_ok[R];
+    int64_t q_off[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        qr[rb] = q0w + 16 * rb + (lane & 15);
+        row_ok[rb] = qr[rb] < p.Nq;
+        q_off[rb] = ((int64_t)b * p.Nq + qr[rb]) * q_row_stride + (int64_t)hq * p.D;
+    }
 
     // Tangent presence: ALL instantiations have every tangent; the others
     // skip the products of the NULL ones.
@@ -125,39 +139,49 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     const bool use_tv = JVP && (ALL || p.tv != nullptr);
 
     // Q (and tQ) as B operands: lane l holds row qr, d = 32*ds + 8*grp + 0..7.
-    x8 qreg[DS], tqreg[DS];
+    x8 qreg[R][DS], tqreg[R][DS];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-        const int d = 32 * ds + 8 * grp;
-        const bool ok = row_ok && d < p.D;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        const u32x4 a = ok ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.q) + q_off + d) : z;
-        qreg[ds] = __builtin_bit_cast(x8, a);
-        if constexpr (JVP) {
-            const u32x4 t = (ok && use_tq)
-                                ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.tq) + q_off + d)
-                                : z;
-            tqreg[ds] = __builtin_bit_cast(x8, t);
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const int d = 32 * ds + 8 * grp;
+            const bool ok = row_ok[rb] && d < p.D;
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            const u32x4 a = ok ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.q) + q_off[rb] + d) : z;
+            qreg[rb][ds] = __builtin_bit_cast(x8, a);
+            if constexpr (JVP) {
+                const u32x4 t = (ok && use_tq)
+                                    ? *reinterpret_cast<const u32x4*>(static_cast<const T*>(p.tq) + q_off[rb] + d)
+                                    : z;
+                tqreg[rb][ds] = __builtin_bit_cast(x8, t);
+            }
         }
-    }
 
     // Key range of the workgroup.
     int key_stop = p.Nk;
     if (p.causal) key_stop = min(p.Nk, max(0, qtile * kBQ + kBQ + diag));
     const int ntiles = (key_stop + kBK - 1) / kBK;
-    const int klim = p.causal ? min(p.Nk - 1, qr + diag) : p.Nk - 1;
+    int klim[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) klim[rb] = p.causal ? min(p.Nk - 1, qr[rb] + diag) : p.Nk - 1;
     const float c = p.scale_log2;
 
     // Row statistics (each lane holds a quarter of its row's keys).  l_run and
     // r_run sum the 16-bit E and H values the products consume, so O is an
     // exact convex combination of V rows and tO = sum_j H_j (v_j - O) / l;
     // l_lse sums the fp32 E for the LSE output.  m_run is in log2 units.
-    float m_run = -__builtin_inff(), l_run = 0.f, r_run = 0.f, l_lse = 0.f;
+    float m_run[R], l_run[R], r_run[R], l_lse[R];
     // Exponent offset: -m_run, or -LSE (log2 units) in the JVP mode (+inf LSE
     // -> P = 0).
-    float nref = 0.f;
-    if constexpr (MODE == FA_JVP) {
-        nref = row_ok ? -p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : -__builtin_inff();
+    float nref[R];
+#pragma unroll
+    for (int rb = 0; rb < R; ++rb) {
+        m_run[rb] = -__builtin_inff();
+        l_run[rb] = r_run[rb] = l_lse[rb] = 0.f;
+        nref[rb] = 0.f;
+        if constexpr (MODE == FA_JVP) {
+            nref[rb] = row_ok[rb] ? -p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr[rb]] * kLog2e : -__builtin_inff();
+        }
     }
 
     // Full tiles (all keys valid, D == DP) take the uniform-address copy.
@@ -171,12 +195,12 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
         return (k0 + kBK > p.Nk) || (p.causal && k0 + kBK - 1 > q0w + diag);
     };
     // A tile's keys are consumed in halves of 32 (key blocks 2h, 2h+1).
-    auto apply_mask = [&](f32x4 (&s)[2], int k0, int h) {
+    auto apply_mask = [&](f32x4 (&s)[2], int k0, int h, int lim) {
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                if (k0 + 16 * (2 * h + i2) + 4 * grp + i > klim) s[i2][i] = -__builtin_inff();
+                if (k0 + 16 * (2 * h + i2) + 4 * grp + i > lim) s[i2][i] = -__builtin_inff();
     };
     auto row_max = [&](const f32x4 (&s)[2]) {
         float mx = s[0][0];
@@ -232,14 +256,16 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
         }
     };
 
-    // S^T (and tS^T) of key blocks 2h, 2h+1 of the tile in buffer bufc; ends
-    // by reading the first V^T operands of the same half.
-    auto scores = [&](auto bufc, int h, f32x4 (&s)[2], f32x4 (&ts)[2]) {
+    // S^T (and tS^T) of key blocks 2h, 2h+1 of the tile in buffer bufc, for
+    // every row block; ends by reading the first V^T operands of the half.
+    auto scores = [&](auto bufc, int h, f32x4 (&s)[R][2], f32x4 (&ts)[R][2]) {
 #pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2) {
-            s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-            ts[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int i2 = 0; i2 < 2; ++i2) {
+                s[rb][i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ts[rb][i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
         for (int st = 0; st < PF && st < NSTEP; ++st) k_load(bufc, h, st);
 #pragma unroll
@@ -248,10 +274,13 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
             if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
             const int i2 = st / DS, ds = st % DS;
             const x8 ka = kring[st % NR];
-            s[i2] = mfma16x16x32(ka, qreg[ds], s[i2]);
-            if constexpr (JVP) {
-                if (use_tq) ts[i2] = mfma16x16x32(ka, tqreg[ds], ts[i2]);
-                if (use_tk) ts[i2] = mfma16x16x32(tkring[st % NR], qreg[ds], ts[i2]);
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                s[rb][i2] = mfma16x16x32(ka, qreg[rb][ds], s[rb][i2]);
+                if constexpr (JVP) {
+                    if (use_tq) ts[rb][i2] = mfma16x16x32(ka, tqreg[rb][ds], ts[rb][i2]);
+                    if (use_tk) ts[rb][i2] = mfma16x16x32(tkring[st % NR], qreg[rb][ds], ts[rb][i2]);
+                }
             }
             if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
         }
@@ -261,48 +290,57 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
 
     // E = exp2(S*c + nref) and H = E * scale * tS, packed to 16 bits; their
     // rounded values are summed into l and r.
-    auto probs = [&](const f32x4 (&s)[2], const f32x4 (&ts)[2], u32x2 (&ew)[2], u32x2 (&hw)[2]) {
+    auto probs = [&](int rb, const f32x4 (&s)[2], const f32x4 (&ts)[2], u32x2 (&ew)[2], u32x2 (&hw)[2]) {
         float esum = 0.f;
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref));
-                const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref));
+                const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref[rb]));
+                const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref[rb]));
                 if constexpr (MODE != FA_JVP) esum += e0 + e1;
                 const unsigned pe = Pk<T>::cvt(e0, e1);
                 ew[i2][j] = pe;
-                l_run = Pk<T>::sum_into(pe, l_run);
+                l_run[rb] = Pk<T>::sum_into(pe, l_run[rb]);
                 if constexpr (JVP) {
                     const unsigned ph = Pk<T>::cvt(e0 * (ts[i2][2 * j] * p.scale), e1 * (ts[i2][2 * j + 1] * p.scale));
                     hw[i2][j] = ph;
-                    r_run = Pk<T>::sum_into(ph, r_run);
+                    r_run[rb] = Pk<T>::sum_into(ph, r_run[rb]);
                 }
             }
-        if constexpr (MODE != FA_JVP) l_lse += esum;
+        if constexpr (MODE != FA_JVP) l_lse[rb] += esum;
     };
 
-    f32x4 u[DB], g[DB];
+    f32x4 u[R][DB], g[R][DB];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        u[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-        g[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            u[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            g[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 
     // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the 32 keys of half h
     // of the tile in buffer bufc.
-    auto pv = [&](auto bufc, int h, const u32x2 (&ew)[2], const u32x2 (&hw)[2]) {
-        const x8 eb = __builtin_bit_cast(x8, u32x4{ew[0][0], ew[0][1], ew[1][0], ew[1][1]});
-        const x8 hb = __builtin_bit_cast(x8, u32x4{hw[0][0], hw[0][1], hw[1][0], hw[1][1]});
+    auto pv = [&](auto bufc, int h, const u32x2 (&ew)[R][2], const u32x2 (&hw)[R][2]) {
+        x8 eb[R], hb[R];
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            eb[rb] = __builtin_bit_cast(x8, u32x4{ew[rb][0][0], ew[rb][0][1], ew[rb][1][0], ew[rb][1][1]});
+            hb[rb] = __builtin_bit_cast(x8, u32x4{hw[rb][0][0], hw[rb][0][1], hw[rb][1][0], hw[rb][1][1]});
+        }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
             if (db + PF < DB) v_load(bufc, h, db + PF);
             if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
             const x8 va = vring[db % NR];
-            u[db] = mfma16x16x32(va, eb, u[db]);
-            if constexpr (JVP) {
-                g[db] = mfma16x16x32(va, hb, g[db]);
-                if (use_tv) g[db] = mfma16x16x32(tvring[db % NR], eb, g[db]);
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                u[rb][db] = mfma16x16x32(va, eb[rb], u[rb][db]);
+                if constexpr (JVP) {
+                    g[rb][db] = mfma16x16x32(va, hb[rb], g[rb][db]);
+                    if (use_tv) g[rb][db] = mfma16x16x32(tvring[db % NR], eb[rb], g[rb][db]);
+                }
             }
             if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
         }
@@ -311,23 +349,23 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     // LAZY: raise the reference of rows whose max grew past m + 2^3 and
     // rescale their state (alpha = 0 for a row leaving m = -inf, whose state
     // is zero).
-    auto rebase = [&](const f32x4 (&s)[2]) {
+    auto rebase = [&](int rb, const f32x4 (&s)[2]) {
         const float mx = row_max(s);
-        const bool upd = mx > m_run + kRescaleThreshold;
+        const bool upd = mx > m_run[rb] + kRescaleThreshold;
         if (__any(upd)) {
-            const float alpha = upd ? fast_exp2(m_run - mx) : 1.f;
-            if (upd) m_run = mx;
-            l_run *= alpha;
-            r_run *= alpha;
-            l_lse *= alpha;
+            const float alpha = upd ? fast_exp2(m_run[rb] - mx) : 1.f;
+            if (upd) m_run[rb] = mx;
+            l_run[rb] *= alpha;
+            r_run[rb] *= alpha;
+            l_lse[rb] *= alpha;
 #pragma unroll
             for (int db = 0; db < DB; ++db)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    u[db][i] *= alpha;
-                    if constexpr (JVP) g[db][i] *= alpha;
+                    u[rb][db][i] *= alpha;
+                    if constexpr (JVP) g[rb][db][i] *= alpha;
                 }
-            nref = m_run == -__builtin_inff() ? 0.f : -m_run;
+            nref[rb] = m_run[rb] == -__builtin_inff() ? 0.f : -m_run[rb];
         }
     };
 
@@ -342,22 +380,27 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
         if (t + 1 < ntiles) issue_side(t + 1, nbuf, std::false_type{});
 #pragma unroll
         for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
-            f32x4 s[2], ts[2];
-            u32x2 ew[2], hw[2] = {u32x2{0u, 0u}, u32x2{0u, 0u}};
+            f32x4 s[R][2], ts[R][2];
+            u32x2 ew[R][2], hw[R][2];
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) hw[rb][0] = hw[rb][1] = u32x2{0u, 0u};
             scores(bufc, h, s, ts);
             if (h == 0 && t + 1 < ntiles) issue_side(t + 1, nbuf, std::true_type{});
-            if (masked) apply_mask(s, k0, h);
-            if constexpr (MODE != FA_JVP) {
-                if constexpr (LAZY) {
-                    rebase(s);
-                } else if (t == 0 && h == 0) {
-                    // Every non-empty row has a valid key among its first 32
-                    // (masks only cut keys off at the end).
-                    m_run = row_max(s);
-                    nref = m_run == -__builtin_inff() ? 0.f : -m_run;
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                if (masked) apply_mask(s[rb], k0, h, klim[rb]);
+                if constexpr (MODE != FA_JVP) {
+                    if constexpr (LAZY) {
+                        rebase(rb, s[rb]);
+                    } else if (t == 0 && h == 0) {
+                        // Every non-empty row has a valid key among its first
+                        // 32 (masks only cut keys off at the end).
+                        m_run[rb] = row_max(s[rb]);
+                        nref[rb] = m_run[rb] == -__builtin_inff() ? 0.f : -m_run[rb];
+                    }
                 }
+                probs(rb, s[rb], ts[rb], ew[rb], hw[rb]);
             }
-            probs(s, ts, ew, hw);
             pv(bufc, h, ew, hw);
         }
     };
@@ -373,46 +416,56 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     if constexpr (MODE != FA_JVP && !LAZY) {
         // Overflow check, made uniform over the workgroup (the rescaling scan
         // needs every wavefront for its tile copies).
-        bool fin = __builtin_isfinite(l_lse) && __builtin_isfinite(r_run);
+        bool fin = true;
 #pragma unroll
-        for (int db = 0; db < DB; ++db)
+        for (int rb = 0; rb < R; ++rb) {
+            fin = fin && __builtin_isfinite(l_lse[rb]) && __builtin_isfinite(r_run[rb]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                fin = fin && __builtin_isfinite(u[db][i]);
-                if constexpr (JVP) fin = fin && __builtin_isfinite(g[db][i]);
-            }
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    fin = fin && __builtin_isfinite(u[rb][db][i]);
+                    if constexpr (JVP) fin = fin && __builtin_isfinite(g[rb][db][i]);
+                }
+        }
         if (__syncthreads_or(!fin)) {
-            if (grp == 0 && row_ok) p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] = __builtin_nanf("");
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb)
+                if (grp == 0 && row_ok[rb]) p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr[rb]] = __builtin_nanf("");
             return;
         }
     }
 
     // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
-    const float l_tot = row_sum4(l_run);
-    const float r_tot = row_sum4(r_run);
-    const float l_lse_tot = row_sum4(l_lse);
-    T* orow = static_cast<T*>(p.o) + q_off;
-    T* torow = static_cast<T*>(p.to) + q_off;
-    const bool empty = !(l_tot > 0.f);
-    const float inv = empty ? 0.f : 1.f / l_tot;
-    const float rl = r_tot * inv;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        const int d = 16 * db + 4 * grp;
-        if (row_ok && d < p.D) {
-            typename V<T>::x4 ov, tv;
+    for (int rb = 0; rb < R; ++rb) {
+        const float l_tot = row_sum4(l_run[rb]);
+        const float r_tot = row_sum4(r_run[rb]);
+        const float l_lse_tot = row_sum4(l_lse[rb]);
+        T* orow = static_cast<T*>(p.o) + q_off[rb];
+        T* torow = static_cast<T*>(p.to) + q_off[rb];
+        const bool empty = !(l_tot > 0.f);
+        const float inv = empty ? 0.f : 1.f / l_tot;
+        const float rl = r_tot * inv;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float o = u[db][e] * inv;
-                ov[e] = (T)o;
-                if constexpr (JVP) tv[e] = (T)(g[db][e] * inv - rl * o);
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + 4 * grp;
+            if (row_ok[rb] && d < p.D) {
+                typename V<T>::x4 ov, tv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float o = u[rb][db][e] * inv;
+                    ov[e] = (T)o;
+                    if constexpr (JVP) tv[e] = (T)(g[rb][db][e] * inv - rl * o);
+                }
+                if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
+                if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
             }
-            if constexpr (MODE != FA_JVP) *reinterpret_cast<typename V<T>::x4*>(orow + d) = ov;
-            if constexpr (JVP) *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
         }
-    }
-    if (MODE != FA_JVP && grp == 0 && row_ok) {
-        p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] = empty ? __builtin_inff() : (m_run + log2f(l_lse_tot)) * kLn2;
+        if (MODE != FA_JVP && grp == 0 && row_ok[rb]) {
+            p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr[rb]] =
+                empty ? __builtin_inff() : (m_run[rb] + log2f(l_lse_tot)) * kLn2;
+        }
     }
 }
 
@@ -444,9 +497,11 @@ __global__ __launch_bounds__(FaTile<DP>::THREADS)
 __attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
 void fa_fixup_kernel(const FaParams p) {
     const FaBlock blk = fa_block(p);
-    const int row = blk.qtile * FaTile<DP>::BQ + (int)threadIdx.x;
+    constexpr int kBQ = fa_rows<DP, MODE>();
+    static_assert(kBQ <= FaTile<DP>::THREADS, "one thread per row checks the marker");
+    const int row = blk.qtile * kBQ + (int)threadIdx.x;
     bool marked = false;
-    if (threadIdx.x < FaTile<DP>::BQ && row < p.Nq)
+    if (threadIdx.x < kBQ && row < p.Nq)
         marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
     if (!__syncthreads_or(marked)) return;
     FA_LDS_BUFFERS(T, DP, MODE);
@@ -502,7 +557,7 @@ int fa_dispatch(int mode, FaParams p, int dtype, hipStream_t stream) {
     KF_REQUIRE(p.q && p.k && p.v && p.o && p.lse && (mode == FA_FWD || p.to), KF_E_INVALID,
                "fa: null pointer");
     const int dp = p.D <= 32 ? 32 : p.D <= 64 ? 64 : p.D <= 128 ? 128 : 256;
-    const int bq = dp > 128 ? FaTile<256>::BQ : FaTile<128>::BQ;
+    const int bq = dp > 128 ? fa_rows<256, FA_FWD_JVP>() : mode == FA_FWD ? fa_rows<128, FA_FWD>() : fa_rows<128, FA_FWD_JVP>();
     p.group = p.Hq / p.Hkv;
     p.n_qtiles = (p.Nq + bq - 1) / bq;
     p.scale_log2 = p.scale * kLog2e;
