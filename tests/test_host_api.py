@@ -43,6 +43,9 @@ def test_fa_cpu_tensors_are_rejected_not_computed():
         fa.flash_attention(q, k, v)
     with pytest.raises(ValueError, match="CUDA"):
         fa.flash_attention_fwd_jvp(q, k, v, None, None, None)
+    lse = torch.zeros(1, 2, 9)
+    with pytest.raises(ValueError, match="CUDA"):
+        fa.flash_attention_backward(q, q, k, v, q, lse)
 
 
 def test_sana_factory_validation():
@@ -82,3 +85,5 @@ def test_fake_impls_for_tracing():
         assert out.shape == q.shape and lse.shape == (1, 2, 9) and lse.dtype == torch.float32
         o, l2, t = fa._fwd_jvp_fake(q, k, k, None, None, None, 0.1, True)
         assert t.shape == q.shape
+        dq, dk, dv = fa._bwd_fake(q, q, k, k, q, lse, 0.1, False)
+        assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
