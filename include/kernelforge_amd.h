@@ -2,13 +2,16 @@
  * kernelforge_amd C ABI.
  *
  * Plain C entry points for the three operator hot paths of KernelForge
- * (RMSNorm, SANA ReLU linear attention, FlashAttention forward/JVP),
- * implemented as hand-written HIP kernels for gfx950 (MI355X).
+ * (RMSNorm, SANA ReLU linear attention with its rotary embedding,
+ * FlashAttention forward / JVP / backward), implemented as hand-written HIP
+ * kernels for gfx950 (MI355X).
  *
  * Conventions shared by every entry point:
  *   - Pointers are device pointers owned by the caller.  The library never
- *     allocates device memory; SANA's cross-split partials live in a caller
- *     supplied workspace whose size is given by kf_linattn_workspace_bytes.
+ *     allocates device memory; SANA's cross-split partials and the FA
+ *     backward's per-row statistics live in caller-supplied workspaces whose
+ *     sizes are given by kf_linattn_workspace_bytes and
+ *     kf_fa_bwd_workspace_bytes.
  *   - Tensors are dense and row-major (the innermost dimension is contiguous)
  *     in the layouts documented per function.
  *   - `stream` is a hipStream_t (NULL = the default stream).  Launches are
@@ -134,6 +137,21 @@ int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
                    int64_t workspace_bytes, int64_t batch, int64_t seq_len,
                    int64_t heads, int64_t dim, int64_t splits, float eps,
                    int in_dtype, int out_dtype, kf_stream_t stream);
+
+/*
+ * Rotary position embedding, in place on the q and k parts of a packed
+ * qkv[batch, seq_len, 3, heads*dim] buffer (v untouched): within each head,
+ * channels (2i, 2i+1) rotate as a complex pair by the angle whose cosine and
+ * sine are cos[n][2i..2i+1], sin[n][2i..2i+1] (fp32 [seq_len][dim]):
+ *   out[2i] = x[2i] cos - x[2i+1] sin,  out[2i+1] = x[2i+1] cos + x[2i] sin,
+ * products and sum rounded in fp32 and the result in the storage type
+ * (dtype KF_F32/F16/BF16).  dim % 8 == 0, qkv 16-byte aligned.  Replaces
+ * apply_rotary_emb(.., use_real_unbind_dim=-2) on q and k in LiteLA.forward
+ * (SANA_LinearAttention/original.py:14-58, 136-138).
+ */
+int kf_rope_packed(void* qkv, const float* cos, const float* sin,
+                   int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
+                   int dtype, kf_stream_t stream);
 
 /* ------------------------------------------------------------------ */
 /* FlashAttention forward and JVP                                      */

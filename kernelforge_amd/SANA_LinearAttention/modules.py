@@ -17,15 +17,20 @@ Data path of ``forward(x[B, N, C])``:
    ``torch.nn.functional.linear``) into the packed ``[B, N, 3, C]`` layout.
 2. ``qk_norm``: RMSNorm over the C channels of each token's q and k, in place
    in the packed buffer (``kf_rmsnorm_fwd_strided``, no copies).
-3. ReLU linear attention (``kf_linattn_fwd``: split states on MFMA, fixed-order
+3. ``rotary_emb = (cos, sin)``: rotary embedding of q and k, in place in the
+   packed buffer (``kf_rope_packed``; original.py:136-138).
+4. ReLU linear attention (``kf_linattn_fwd``: split states on MFMA, fixed-order
    split reduction, MFMA output contraction), fp32 arithmetic.
-4. ``y = out @ Wproj^T + b`` -- library GEMM with the bias in its epilogue.
+5. ``y = out @ Wproj^T + b`` -- library GEMM with the bias in its epilogue.
 
 Numerics: the attention always runs with the reference's ``fp32_attention``
 semantics (ReLU on the stored 16-bit values, products and sums in fp32), so
-``fp32_attention = True`` needs no separate path.  Rotary embeddings
-(``rotary_emb``) are not implemented and raise ``NotImplementedError``; the
-reference sends them to its eager torch path.
+``fp32_attention = True`` needs no separate path.  The reference sends
+``rotary_emb`` through its eager torch path; here it is one more in-place
+kernel on the packed buffer, rounded the way the eager path rounds.
+
+``apply_rotary_emb`` (original.py:14-58) is exported as well, as the torch
+helper it is in the reference (device tensors only); LiteLA does not call it.
 """
 
 from __future__ import annotations
@@ -36,6 +41,38 @@ from torch import nn
 from .. import _lib
 from ..rmsnorm.custom import RMSNorm, rms_norm_rows_
 from .custom import THREADS, linear_attention
+
+def apply_rotary_emb(x: torch.Tensor, freqs_cis, use_real: bool = True, use_real_unbind_dim: int = -1):
+    """Rotary embedding with the reference's signature (SANA_LinearAttention/original.py:14-58).
+
+    ``use_real``: ``freqs_cis = (cos, sin)`` of ``[S, D]``; channel pairs
+    (2i, 2i+1) run along dim -2 of a ``[B, H, D, S]`` x (``use_real_unbind_dim
+    = -2``, SANA) or along the last dim of a ``[B, H, S, D]`` x (-1) and rotate
+    as ``(a, b) -> (a cos - b sin, b cos + a sin)`` with fp32 products and sum,
+    rounded to x's dtype.  ``use_real=False``: complex ``freqs_cis`` of
+    ``[B or 1, S, D/2]`` multiplies the pairs of a ``[B, S, H, D]`` x.
+    """
+    _lib.require_gpu(x)
+    if not use_real:
+        xf = x.float()
+        z = torch.complex(xf[..., 0::2], xf[..., 1::2]) * freqs_cis.unsqueeze(2)
+        return torch.stack((z.real, z.imag), dim=-1).flatten(-2).to(x.dtype)
+    cos, sin = (t.to(x.device).float() for t in freqs_cis)
+    if use_real_unbind_dim == -2:
+        a, b = x[..., 0::2, :].float(), x[..., 1::2, :].float()
+        cos, sin = cos.T, sin.T
+        c_re, c_im, s_re, s_im = cos[0::2], cos[1::2], sin[0::2], sin[1::2]
+        stack_dim, flat = -2, (-3, -2)
+    elif use_real_unbind_dim == -1:
+        a, b = x[..., 0::2].float(), x[..., 1::2].float()
+        c_re, c_im, s_re, s_im = cos[..., 0::2], cos[..., 1::2], sin[..., 0::2], sin[..., 1::2]
+        stack_dim, flat = -1, (-2, -1)
+    else:
+        raise ValueError(f"`use_real_unbind_dim={use_real_unbind_dim}` but should be -1 or -2.")
+    re = a * c_re + (-b) * s_re
+    im = b * c_im + a * s_im
+    return torch.stack((re, im), dim=stack_dim).flatten(*flat).to(x.dtype)
+
 
 # torch dtype -> reference dtype string (SANA_LinearAttention/custom.py:16-20).
 TORCH_DTYPES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float"}
@@ -102,13 +139,27 @@ class LiteLA(nn.Module):
             self.q_norm = nn.Identity()
             self.k_norm = nn.Identity()
 
-    def _packed_qkv(self, x: torch.Tensor) -> torch.Tensor:
+    def _packed_qkv(self, x: torch.Tensor, rotary_emb=None) -> torch.Tensor:
         B, N, C = x.shape
         qkv = torch.nn.functional.linear(x, self.qkv.weight, self.qkv.bias).reshape(B, N, 3, C)
         if self.qk_norm:
             rms_norm_rows_(qkv[:, :, 0], self.q_norm.weight.detach().to(qkv.dtype), self.q_norm.eps)
             rms_norm_rows_(qkv[:, :, 1], self.k_norm.weight.detach().to(qkv.dtype), self.k_norm.eps)
+        if rotary_emb is not None:
+            self._rotate_(qkv, rotary_emb)
         return qkv
+
+    def _rotate_(self, qkv: torch.Tensor, rotary_emb) -> None:
+        """q and k of the packed qkv rotated in place (original.py:136-138)."""
+        B, N, _, C = qkv.shape
+        if not isinstance(rotary_emb, (tuple, list)) or len(rotary_emb) != 2:
+            raise ValueError("rotary_emb must be a (cos, sin) pair of [N, head_dim] tensors")
+        cos, sin = (t.detach().to(device=qkv.device, dtype=torch.float32).contiguous() for t in rotary_emb)
+        if cos.shape != (N, self.dim) or sin.shape != (N, self.dim):
+            raise ValueError(f"rotary_emb tensors must be [{N}, {self.dim}], got {tuple(cos.shape)}, {tuple(sin.shape)}")
+        rc = _lib.load().kf_rope_packed(_lib.ptr(qkv), _lib.ptr(cos), _lib.ptr(sin), B, N, self.heads, self.dim,
+                                        _lib.kf_dtype(qkv.dtype), _lib.stream_of(qkv))
+        _lib.check(rc, "kf_rope_packed")
 
     def _attention(self, qkv: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
         # The kernel rounds its fp32 result straight to `dtype` (round to
@@ -117,12 +168,10 @@ class LiteLA(nn.Module):
 
     def forward(self, x: torch.Tensor, mask=None, HW=None, rotary_emb=None, block_id=None,
                 block_mask=None) -> torch.Tensor:
-        if rotary_emb is not None:
-            raise NotImplementedError("rotary embeddings are not implemented by the gfx950 LiteLA path")
         if x.dim() != 3 or x.shape[-1] != self.in_dim:
             raise ValueError(f"x must be [B, N, {self.in_dim}], got {tuple(x.shape)}")
         _lib.require_gpu(x)
-        out = self._attention(self._packed_qkv(x), x.dtype)
+        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         return self.proj(out)
 
 
@@ -149,11 +198,9 @@ class CustomLiteLA(LiteLA):
             raise ValueError(f"expected LiteLA dtype {self.dtype}, got {x.dtype}")
 
     def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
-        if rotary_emb is not None:
-            raise NotImplementedError("rotary embeddings are not implemented by the gfx950 LiteLA path")
         self._validate_input(x)
         _lib.require_gpu(x)
-        out = self._attention(self._packed_qkv(x), x.dtype)
+        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         return self.proj(out)
 
 
@@ -171,11 +218,9 @@ class JointLiteLA(CustomLiteLA):
                          norm_eps=norm_eps)
 
     def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
-        if rotary_emb is not None:
-            raise NotImplementedError("rotary embeddings are not implemented by the gfx950 LiteLA path")
         self._validate_input(x)
         _lib.require_gpu(x)
-        out = self._attention(self._packed_qkv(x), x.dtype)
+        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         bias = self.proj.bias
         if bias is None:
             bias = torch.zeros(self.out_dim, device=x.device, dtype=x.dtype)

@@ -1,8 +1,9 @@
 """GPU parity of the LiteLA modules and the in-place strided RMSNorm (qk_norm).
 
-Modules: SANA_LinearAttention/original.py:65-145 (LiteLA), custom.py:391-454
-(CustomLiteLA), custom.py:526-592 (JointLiteLA), custom.py:83-85
-(qkv_projection).  The oracle (oracle/sana.py:lite_la_forward) restates
+Modules: SANA_LinearAttention/original.py:65-145 (LiteLA, with the rotary
+embedding of :136-138), custom.py:391-454 (CustomLiteLA), custom.py:526-592
+(JointLiteLA), custom.py:83-85 (qkv_projection), original.py:14-58
+(apply_rotary_emb).  The oracle (oracle/sana.py:lite_la_forward) restates
 original.py:119-145 on the CPU with the fp32 attention; the projected qkv is
 rounded to the module dtype the way the GPU GEMM's 16-bit output is.
 """
@@ -11,7 +12,8 @@ import pytest
 import torch
 
 from kernelforge_amd.rmsnorm.custom import rms_norm_rows_
-from kernelforge_amd.SANA_LinearAttention import CustomLiteLA, JointLiteLA, LiteLA, qkv_projection
+from kernelforge_amd import _lib
+from kernelforge_amd.SANA_LinearAttention import CustomLiteLA, JointLiteLA, LiteLA, apply_rotary_emb, qkv_projection
 from oracle import rmsnorm as orms
 from oracle import sana as osana
 
@@ -19,11 +21,18 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _module_ref(m, x, qk_norm):
+def _module_ref(m, x, qk_norm, rotary_emb=None):
     return osana.lite_la_forward(
         x.cpu(), m.qkv.weight, m.qkv.bias, m.proj.weight, m.proj.bias, m.heads, m.eps,
         m.q_norm.weight if qk_norm else None, m.k_norm.weight if qk_norm else None,
-        m.q_norm.eps if qk_norm else 1e-5, qkv_dtype=x.dtype)
+        m.q_norm.eps if qk_norm else 1e-5, qkv_dtype=x.dtype, rotary_emb=rotary_emb)
+
+
+def _rope_tables(N, D, seed=4):
+    """cos/sin [N, D] of per-pair angles (equal on channels 2i, 2i+1)."""
+    g = torch.Generator().manual_seed(seed)
+    theta = (torch.rand(N, D // 2, generator=g) * 6.0 - 3.0).repeat_interleave(2, dim=-1)
+    return torch.cos(theta), torch.sin(theta)
 
 
 def _close(got, ref, tol=2e-2):
@@ -63,8 +72,55 @@ def test_custom_and_joint_modules(cls):
         m(x[:, :-1])
     with pytest.raises(ValueError, match="expected LiteLA dtype"):
         m(x.float())
-    with pytest.raises(NotImplementedError):
+    rot = _rope_tables(N, 32)
+    _close(m(x, rotary_emb=rot), _module_ref(m, x, True, rot))
+    with pytest.raises(ValueError, match="rotary_emb"):
         m(x, rotary_emb=(torch.ones(1), torch.ones(1)))
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+def test_rope_packed_matches_oracle_bitwise(dtype):
+    """kf_rope_packed against the oracle's rotation of the packed qkv: the same
+    two fp32 products, one fp32 sum and one rounding, so identical bits."""
+    B, N, H, D = 2, 37, 5, 32
+    g = torch.Generator().manual_seed(7)
+    qkv = torch.randn(B, N, 3, H * D, generator=g).to(dtype)
+    cos, sin = _rope_tables(N, D)
+    dev, dcos, dsin = qkv.to(DEV), cos.to(DEV), sin.to(DEV)  # kept alive across the launch
+    rc = _lib.load().kf_rope_packed(_lib.ptr(dev), _lib.ptr(dcos), _lib.ptr(dsin), B, N, H, D,
+                                    _lib.kf_dtype(dtype), _lib.stream_of(dev))
+    _lib.check(rc, "kf_rope_packed")
+    torch.testing.assert_close(dev.cpu(), osana.rope_packed(qkv, cos, sin, H), atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("qk_norm", (False, True))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_litela_rotary_matches_reference_forward(qk_norm, dtype):
+    torch.manual_seed(0)
+    B, N, C = 2, 300, 8 * 32
+    m = LiteLA(C, C, qk_norm=qk_norm).to(DEV, dtype)
+    x = torch.randn(B, N, C, generator=torch.Generator().manual_seed(1)).to(dtype).to(DEV)
+    rot = _rope_tables(N, 32)
+    out = m(x, rotary_emb=rot)
+    _close(out, _module_ref(m, x, qk_norm, rot))
+    assert not torch.allclose(out, m(x), atol=1e-2)
+
+
+def test_apply_rotary_emb_helper():
+    """The exported helper matches the oracle's apply_rotary_emb for both pair
+    layouts and the complex form."""
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(2, 3, 32, 10, generator=g).to(torch.bfloat16)
+    cos, sin = _rope_tables(10, 32)
+    for dim, xx in ((-2, x), (-1, x.transpose(-1, -2).contiguous())):
+        got = apply_rotary_emb(xx.to(DEV), (cos.to(DEV), sin.to(DEV)), use_real_unbind_dim=dim)
+        torch.testing.assert_close(got.cpu(), osana.apply_rotary_emb(xx, (cos, sin), use_real_unbind_dim=dim),
+                                   atol=0, rtol=0)
+    theta = torch.rand(1, 10, 16, generator=g)
+    freqs = torch.polar(torch.ones_like(theta), theta)
+    xs = x.permute(0, 3, 1, 2).contiguous()
+    got = apply_rotary_emb(xs.to(DEV), freqs.to(DEV), use_real=False)
+    torch.testing.assert_close(got.cpu(), osana.apply_rotary_emb(xs, freqs, use_real=False), atol=1e-2, rtol=1e-2)
 
 
 def test_module_validation():

@@ -153,6 +153,92 @@ def test_lite_la_forward_glue():
     torch.testing.assert_close(got, att * d + bias, rtol=1e-6, atol=1e-6)
 
 
+
+def _angles(S, D, g):
+    """Per-token, per-pair angles: cos/sin [S, D] with equal values on 2i, 2i+1."""
+    theta = torch.rand(S, D // 2, generator=g, dtype=torch.float64) * 6.0 - 3.0
+    rep = theta.repeat_interleave(2, dim=-1)
+    return theta, torch.cos(rep), torch.sin(rep)
+
+
+def test_rotary_closed_forms():
+    """apply_rotary_emb (SANA_LinearAttention/original.py:14-58) pinned by the
+    mathematics: zero angle is the identity, a quarter turn maps (a, b) to
+    (-b, a), equal pair angles are a complex multiplication by e^{i theta}
+    (fp64), rotations preserve each pair's norm and compose additively, and the
+    complex-frequency path agrees with the (cos, sin) path."""
+    g = torch.Generator().manual_seed(11)
+    B, H, D, S = 2, 3, 8, 7
+    x = torch.randn(B, H, D, S, generator=g, dtype=torch.float64)   # SANA layout [B, H, D, S]
+    one, zero = torch.ones(S, D, dtype=torch.float64), torch.zeros(S, D, dtype=torch.float64)
+    assert torch.equal(osana.apply_rotary_emb(x, (one, zero), use_real_unbind_dim=-2), x)
+    quarter = osana.apply_rotary_emb(x, (zero, one), use_real_unbind_dim=-2)
+    assert torch.equal(quarter[:, :, 0::2], -x[:, :, 1::2]) and torch.equal(quarter[:, :, 1::2], x[:, :, 0::2])
+    theta, cos, sin = _angles(S, D, g)
+    got = osana.apply_rotary_emb(x, (cos, sin), use_real_unbind_dim=-2)
+    z = torch.complex(x[:, :, 0::2], x[:, :, 1::2]) * torch.polar(torch.ones_like(theta), theta).T
+    torch.testing.assert_close(got[:, :, 0::2], z.real, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(got[:, :, 1::2], z.imag, rtol=1e-12, atol=1e-12)
+    norm = lambda t: t[:, :, 0::2] ** 2 + t[:, :, 1::2] ** 2
+    torch.testing.assert_close(norm(got), norm(x), rtol=1e-12, atol=1e-12)
+    theta2, cos2, sin2 = _angles(S, D, g)
+    both = osana.apply_rotary_emb(got, (cos2, sin2), use_real_unbind_dim=-2)
+    rep = (theta + theta2).repeat_interleave(2, dim=-1)
+    direct = osana.apply_rotary_emb(x, (torch.cos(rep), torch.sin(rep)), use_real_unbind_dim=-2)
+    torch.testing.assert_close(both, direct, rtol=1e-12, atol=1e-12)
+    # the last-dim layout [B, H, S, D] is the same rotation, transposed
+    last = osana.apply_rotary_emb(x.transpose(-1, -2), (cos, sin), use_real_unbind_dim=-1)
+    torch.testing.assert_close(last, got.transpose(-1, -2), rtol=0, atol=0)
+    # complex frequencies [1, S, D/2] on a [B, S, H, D] tensor
+    xs = x.permute(0, 3, 1, 2)
+    cplx = osana.apply_rotary_emb(xs, torch.polar(torch.ones_like(theta), theta)[None], use_real=False)
+    torch.testing.assert_close(cplx, got.permute(0, 3, 1, 2), rtol=1e-12, atol=1e-12)
+
+
+def test_rotary_packed_layout_and_rounding():
+    """rope_packed rotates q and k of the packed [B, N, 3, C] qkv per head and
+    leaves v alone; a quarter turn moves channel h*D + 2i of token n to
+    h*D + 2i + 1 of the same token and head.  In 16 bits the result is the
+    fp32 value rounded once (round to nearest even)."""
+    B, N, H, D = 1, 4, 3, 8
+    C = H * D
+    qkv = torch.zeros(B, N, 3, C, dtype=torch.float64)
+    qkv[0, 2, 0, 1 * D + 4] = 1.0      # q, token 2, head 1, pair 2 (real part)
+    qkv[0, 1, 1, 2 * D + 7] = 2.0      # k, token 1, head 2, pair 3 (imaginary part)
+    qkv[0, 3, 2, 5] = 3.0              # v is not rotated
+    zero, one = torch.zeros(N, D, dtype=torch.float64), torch.ones(N, D, dtype=torch.float64)
+    out = osana.rope_packed(qkv, zero, one, H)
+    want = torch.zeros_like(qkv)
+    want[0, 2, 0, 1 * D + 5] = 1.0     # (a, b) -> (-b, a): real 1 -> imaginary 1
+    want[0, 1, 1, 2 * D + 6] = -2.0    # imaginary 2 -> real -2
+    want[0, 3, 2, 5] = 3.0
+    assert torch.equal(out, want)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 5, 3, C, generator=g).to(torch.bfloat16)
+    _, cos, sin = _angles(5, D, g)
+    got = osana.rope_packed(x, cos.float(), sin.float(), H)
+    exact = osana.rope_packed(x.double(), cos.float().double(), sin.float().double(), H)
+    # one rounding of a value computed with two fp32 products and one fp32 sum
+    torch.testing.assert_close(got.double(), exact.to(torch.bfloat16).double(), rtol=2 ** -7, atol=1e-6)
+    assert torch.equal(got[:, :, 2], x[:, :, 2])
+
+
+def test_lite_la_forward_rotary():
+    """LiteLA.forward applies the rotary embedding to q and k after the norm
+    and before the attention (SANA_LinearAttention/original.py:129-138)."""
+    g = torch.Generator().manual_seed(9)
+    B, N, H, D = 1, 12, 2, 8
+    C = H * D
+    x = torch.randn(B, N, C, generator=g)
+    eye = torch.eye(C)
+    w_qkv = torch.cat([eye, 2 * eye, 3 * eye])
+    _, cos, sin = _angles(N, D, g)
+    got = osana.lite_la_forward(x, w_qkv, None, eye, None, H, 1e-15, rotary_emb=(cos.float(), sin.float()))
+    qkv = osana.rope_packed(torch.stack((x, 2 * x, 3 * x), dim=2), cos.float(), sin.float(), H)
+    torch.testing.assert_close(got, osana.linear_attention(qkv, H, D), rtol=1e-6, atol=1e-6)
+    plain = osana.lite_la_forward(x, w_qkv, None, eye, None, H, 1e-15)
+    assert not torch.allclose(got, plain, rtol=1e-3)
+
 # ---------------------------------------------------------------------------
 # FlashAttention forward / JVP
 # ---------------------------------------------------------------------------
