@@ -9,19 +9,20 @@
 // (LiteLA.forward, :124-134), out[b][t][h*D + r].
 //
 // Pipeline (D = 32, bf16/f16 input):
-//   1. linattn_state_kernel   grid (splits, ceil(H/2), B): each workgroup streams
+//   1. linattn_state_kernel   grid (ceil(H/2), splits, B): each workgroup streams
 //      one sequence split of two adjacent heads (128 contiguous bytes of K and of
 //      V per token) through LDS and accumulates S with v_mfma_f32_32x32x16; the
 //      token-major operands are read with ds_read_b64_tr_b16.  z accumulates on
 //      the VALU from the same registers.  Partials [B][H][splits][D+1][D] fp32.
 //   2. linattn_reduce_kernel  one thread per state element: sums the partials in
 //      split order (fixed order: deterministic, no atomics).
-//   3. linattn_out_kernel     grid (ceil(N/128), ceil(H/4), B): one wavefront per
+//   3. linattn_out_kernel     grid (ceil(H/4), ceil(N/64), B): one wavefront per
 //      head keeps S and z in registers as hi+lo 16-bit pairs (so the products
-//      carry ~16 mantissa bits of the fp32 state) and streams relu(q) straight
-//      from HBM as the B operand of v_mfma_f32_16x16x32; z is a third A operand
-//      whose rows all equal z, so the denominator lands in the same lanes as the
-//      numerator.  No LDS, no barriers.
+//      carry ~16 mantissa bits of the fp32 state); relu(q) of 64 tokens x 4
+//      heads arrives with whole-line loads, is staged in LDS and read back as
+//      the B operand of v_mfma_f32_16x16x32; z is a third A operand whose rows
+//      all equal z, so the denominator lands in the same lanes as the
+//      numerator.  The normalised rows leave through LDS as whole-line stores.
 // Other head dims (128 % D == 0) and fp32 input take a VALU path with the same
 // three stages and the same fixed-order split reduction.
 #include "kf_common.h"
