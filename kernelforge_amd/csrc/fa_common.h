@@ -92,13 +92,13 @@ template <int CH> __device__ __forceinline__ int swz(int r) {
 
 // Async copy of one [BK][DP] tile (keys k0.., one kv head) into LDS.  A tile
 // is NI = BK*DP/512 copy instructions of 64 lanes x 16 B (RPI rows each);
-// wavefront w issues instructions w, w + WAVES, ...
-template <typename T, int DP>
+// wavefront w of the W issuing ones issues instructions w, w + W, ...
+template <typename T, int DP, int W = FaTile<DP>::WAVES>
 __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_stride, int keys_valid,
                                           int D, int wave, int lane) {
     constexpr int CH = DP / 8;
     constexpr int RPI = 64 / CH;
-    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
+    constexpr int NI = FaTile<DP>::BK / RPI;
 #pragma unroll
     for (int j = 0; j < (NI + W - 1) / W; ++j) {
         const int i = wave + j * W;
@@ -115,12 +115,12 @@ __device__ __forceinline__ void load_tile(T* tile, const T* g, int64_t row_strid
 }
 
 // Byte offset, within a full tile, of the 16-byte chunk lane `lane` copies.
-// The rows a lane copies are wave*RPI + lane/CH plus multiples of WAVES*RPI;
+// The rows a lane copies are wave*RPI + lane/CH plus multiples of W*RPI;
 // when that is a multiple of 16 (full_tile_shortcut), their swizzle (a
 // function of row % 16) is the same for every instruction and one offset
 // serves them all.
-template <int DP> constexpr bool full_tile_shortcut() {
-    return (FaTile<DP>::WAVES * (64 / (DP / 8))) % 16 == 0;
+template <int DP, int W = FaTile<DP>::WAVES> constexpr bool full_tile_shortcut() {
+    return (W * (64 / (DP / 8))) % 16 == 0;
 }
 template <typename T, int DP>
 __device__ __forceinline__ uint32_t full_tile_lane_offset(int64_t row_stride, int wave, int lane) {
@@ -133,13 +133,13 @@ __device__ __forceinline__ uint32_t full_tile_lane_offset(int64_t row_stride, in
 
 // Async copy of a tile whose 64 rows are all valid and whose rows hold exactly
 // DP elements: a uniform base per instruction plus one per-lane offset.
-template <typename T, int DP>
+template <typename T, int DP, int W = FaTile<DP>::WAVES>
 __device__ __forceinline__ void load_tile_full(T* tile, const T* g, int64_t row_stride, uint32_t voff,
                                                int wave) {
     constexpr int CH = DP / 8;
     constexpr int RPI = 64 / CH;
-    constexpr int NI = FaTile<DP>::BK / RPI, W = FaTile<DP>::WAVES;
-    static_assert(full_tile_shortcut<DP>(), "one lane offset serves every instruction");
+    constexpr int NI = FaTile<DP>::BK / RPI;
+    static_assert(full_tile_shortcut<DP, W>(), "one lane offset serves every instruction");
 #pragma unroll
     for (int j = 0; j < (NI + W - 1) / W; ++j) {
         const int i = wave + j * W;

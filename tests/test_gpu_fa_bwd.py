@@ -162,3 +162,30 @@ def test_baseline_config_backward(causal):
     for name, actual, r in zip(("dq", "dk", "dv"), grads, ref):
         torch.testing.assert_close(actual.float(), r, atol=2e-2, rtol=2e-2, msg=lambda m: f"{name}: {m}")
         assert ((actual.float() - r).norm() / r.norm()).item() < 1e-2
+
+
+def test_backward_graph_replay():
+    """The backward launches (dq and dkdv kernels, torch-allocated workspace)
+    replay from a captured HIP graph with the eager result, also after the
+    cotangent changes in place; the program's own eager work runs between
+    replays."""
+    case = (1, 70, 90, 4, 2, 64, True, None)
+    q, k, v, cot = make_inputs(case, torch.bfloat16)
+    out, lse = flash_attention(q, k, v, causal=True, return_lse=True)
+    expected = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(captured, expected):
+            torch.testing.assert_close(c, e, atol=0, rtol=0)
+        flash_attention(q, k, v)  # unrelated eager work between replays
+    cot.mul_(0.5)
+    expected = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, e in zip(captured, expected):
+            torch.testing.assert_close(c, e, atol=0, rtol=0)
