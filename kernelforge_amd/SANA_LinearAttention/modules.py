@@ -35,6 +35,8 @@ helper it is in the reference (device tensors only); LiteLA does not call it.
 
 from __future__ import annotations
 
+from typing import Optional
+
 import torch
 from torch import nn
 
@@ -103,6 +105,43 @@ def qkv_projection(batch: int, seq_len: int, channels: int, dtype: str = "bfloat
     return _QKVProjection(batch, seq_len, channels, dtypes[dtype])
 
 
+def _project_qkv(x: torch.Tensor, weight: torch.Tensor, bias, q_norm_weight, k_norm_weight,
+                 norm_eps: float) -> torch.Tensor:
+    """``x[B, N, C] -> qkv[B, N, 3, C]``: library GEMM, then the optional q/k
+    RMSNorm over C in place in the packed buffer (original.py:122-130)."""
+    B, N, C = x.shape
+    qkv = torch.nn.functional.linear(x, weight, bias).reshape(B, N, 3, C)
+    if q_norm_weight is not None:
+        rms_norm_rows_(qkv[:, :, 0], q_norm_weight.detach().to(qkv.dtype), norm_eps)
+        rms_norm_rows_(qkv[:, :, 1], k_norm_weight.detach().to(qkv.dtype), norm_eps)
+    return qkv
+
+
+def _project_out_joint(out: torch.Tensor, weight: torch.Tensor, bias) -> torch.Tensor:
+    """``out[B, N, C] @ W^T + b`` with the bias added in the GEMM (custom.py:469-523)."""
+    B, N, C = out.shape
+    if bias is None:
+        bias = torch.zeros(weight.shape[0], device=out.device, dtype=out.dtype)
+    return torch.addmm(bias.to(out.dtype), out.reshape(-1, C), weight.t()).reshape(B, N, weight.shape[0])
+
+
+@torch.library.custom_op("kernelforge_amd::joint_litela_forward", mutates_args=(), device_types="cuda")
+def _joint_litela_op(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],
+                     proj_weight: torch.Tensor, proj_bias: Optional[torch.Tensor],
+                     q_norm_weight: Optional[torch.Tensor], k_norm_weight: Optional[torch.Tensor],
+                     heads: int, dim: int, eps: float, norm_eps: float) -> torch.Tensor:
+    """JointLiteLA's forward as one opaque operator (SANA_LinearAttention/custom.py:885-898)."""
+    _lib.require_gpu(x)
+    qkv = _project_qkv(x, qkv_weight, qkv_bias, q_norm_weight, k_norm_weight, norm_eps)
+    return _project_out_joint(linear_attention(qkv, heads, dim, eps, x.dtype), proj_weight, proj_bias)
+
+
+@_joint_litela_op.register_fake
+def _joint_litela_op_fake(x, qkv_weight, qkv_bias, proj_weight, proj_bias, q_norm_weight, k_norm_weight,
+                          heads, dim, eps, norm_eps):
+    return x.new_empty((*x.shape[:-1], proj_weight.shape[0]))
+
+
 class LiteLA(nn.Module):
     """Lightweight ReLU linear attention (SANA_LinearAttention/original.py:65-145).
 
@@ -139,12 +178,14 @@ class LiteLA(nn.Module):
             self.q_norm = nn.Identity()
             self.k_norm = nn.Identity()
 
+    def _norm_weights(self):
+        if not self.qk_norm:
+            return None, None, 1e-5
+        return self.q_norm.weight, self.k_norm.weight, self.q_norm.eps
+
     def _packed_qkv(self, x: torch.Tensor, rotary_emb=None) -> torch.Tensor:
-        B, N, C = x.shape
-        qkv = torch.nn.functional.linear(x, self.qkv.weight, self.qkv.bias).reshape(B, N, 3, C)
-        if self.qk_norm:
-            rms_norm_rows_(qkv[:, :, 0], self.q_norm.weight.detach().to(qkv.dtype), self.q_norm.eps)
-            rms_norm_rows_(qkv[:, :, 1], self.k_norm.weight.detach().to(qkv.dtype), self.k_norm.eps)
+        qn, kn, norm_eps = self._norm_weights()
+        qkv = _project_qkv(x, self.qkv.weight, self.qkv.bias, qn, kn, norm_eps)
         if rotary_emb is not None:
             self._rotate_(qkv, rotary_emb)
         return qkv
@@ -221,8 +262,87 @@ class JointLiteLA(CustomLiteLA):
         self._validate_input(x)
         _lib.require_gpu(x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        bias = self.proj.bias
-        if bias is None:
-            bias = torch.zeros(self.out_dim, device=x.device, dtype=x.dtype)
-        return torch.addmm(bias.to(x.dtype), out.reshape(-1, self.in_dim), self.proj.weight.t()).reshape(
-            x.shape[0], x.shape[1], self.out_dim)
+        return _project_out_joint(out, self.proj.weight, self.proj.bias)
+
+
+class CustomOpJointLiteLA(JointLiteLA):
+    """JointLiteLA exposed to Dynamo as one opaque custom operator
+    (``kernelforge_amd::joint_litela_forward``; SANA_LinearAttention/custom.py:
+    885-918), so ``torch.compile(..., fullgraph=True)`` traces it without
+    graph breaks.  With ``rotary_emb`` the module falls back to
+    ``JointLiteLA.forward``, as the reference does."""
+
+    def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
+        if rotary_emb is not None:
+            return super().forward(x, mask, HW, rotary_emb, block_id, block_mask)
+        self._validate_input(x)
+        _lib.require_gpu(x)
+        qn, kn, norm_eps = self._norm_weights()
+        return _joint_litela_op(x, self.qkv.weight, self.qkv.bias, self.proj.weight, self.proj.bias, qn, kn,
+                                self.heads, self.dim, self.eps, norm_eps)
+
+
+class CUDAGraphJointLiteLA:
+    """Fixed-shape HIP graph replay of a JointLiteLA (SANA_LinearAttention/
+    custom.py:923-945): three warm-up calls on a side stream, one captured
+    call, then ``__call__`` copies x into the static input (that copy is part
+    of the measured cost) and replays.  The returned tensor is the graph's
+    static output, overwritten by the next call."""
+
+    def __init__(self, module: JointLiteLA):
+        self.module = module
+        self.static_input = torch.empty(module.input_shape, device=module.proj.weight.device, dtype=module.dtype)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), torch.inference_mode():
+            for _ in range(3):
+                module(self.static_input)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.inference_mode(), torch.cuda.graph(self.graph):
+            self.static_output = module(self.static_input)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        self.static_input.copy_(x)
+        self.graph.replay()
+        return self.static_output
+
+
+# The reference's single-shape fused module (SANA_LinearAttention/custom.py:
+# 595-603, 812-861): B=1, N=1024, C=1152, 36 heads of 32, bf16.
+GROUPED_SHAPE = (1, 1024, 1152)
+GROUPED_HEADS, GROUPED_DIM = 36, 32
+
+
+class GroupedFull64QOutLiteLA(JointLiteLA):
+    """The reference's shape-specialised LiteLA (SANA_LinearAttention/custom.py:812-861),
+    with its constructor checks: exactly B=1, N=1024, C=1152, H=36, D=32, bf16,
+    ``qk_norm=False``, ``use_bias=False``, and no ``rotary_emb``.  The reference
+    fuses the QKV projection into its attention kernels for this one shape;
+    here it runs JointLiteLA's pipeline, whose attention kernels already
+    stream the packed qkv once."""
+
+    def __init__(self, *args, **kwargs):
+        batch, seq_len, dtype = kwargs.get("batch"), kwargs.get("seq_len"), kwargs.get("dtype")
+        dim = kwargs.get("dim", GROUPED_DIM)
+        heads = kwargs.get("heads")
+        in_dim = args[0] if args else kwargs.get("in_dim")
+        out_dim = args[1] if len(args) > 1 else kwargs.get("out_dim")
+        if ((batch, seq_len, in_dim, out_dim) != (*GROUPED_SHAPE, GROUPED_SHAPE[2])
+                or (heads is not None and heads != GROUPED_HEADS) or dtype != torch.bfloat16
+                or dim != GROUPED_DIM or kwargs.get("qk_norm", False) or kwargs.get("use_bias", False)):
+            raise ValueError("GroupedFull64QOutLiteLA requires exactly B=1,N=1024,C=1152,H=36,D=32, "
+                             "bf16, qk_norm=False, and use_bias=False")
+        super().__init__(*args, **kwargs)
+
+    def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
+        if rotary_emb is not None:
+            raise ValueError("GroupedFull64QOutLiteLA requires rotary_emb=None")
+        return super().forward(x, mask, HW, None, block_id, block_mask)
+
+
+def optimized_joint_litela(in_dim: int, out_dim: int, **kwargs) -> JointLiteLA:
+    """The module the reference picks for a shape (SANA_LinearAttention/custom.py:864-868)."""
+    shape = (kwargs.get("batch"), kwargs.get("seq_len"), in_dim)
+    module_cls = GroupedFull64QOutLiteLA if shape == GROUPED_SHAPE else JointLiteLA
+    return module_cls(in_dim, out_dim, **kwargs)

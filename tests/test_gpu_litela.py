@@ -3,7 +3,10 @@
 Modules: SANA_LinearAttention/original.py:65-145 (LiteLA, with the rotary
 embedding of :136-138), custom.py:391-454 (CustomLiteLA), custom.py:526-592
 (JointLiteLA), custom.py:83-85 (qkv_projection), original.py:14-58
-(apply_rotary_emb).  The oracle (oracle/sana.py:lite_la_forward) restates
+(apply_rotary_emb), custom.py:864-945 (CustomOpJointLiteLA,
+CUDAGraphJointLiteLA, optimized_joint_litela) and custom.py:812-861
+(GroupedFull64QOutLiteLA, checked at its one shape).  The custom-operator and
+graph tests follow SANA_LinearAttention/test.py:120-150.  The oracle (oracle/sana.py:lite_la_forward) restates
 original.py:119-145 on the CPU with the fp32 attention; the projected qkv is
 rounded to the module dtype the way the GPU GEMM's 16-bit output is.
 """
@@ -13,7 +16,9 @@ import torch
 
 from kernelforge_amd.rmsnorm.custom import rms_norm_rows_
 from kernelforge_amd import _lib
-from kernelforge_amd.SANA_LinearAttention import CustomLiteLA, JointLiteLA, LiteLA, apply_rotary_emb, qkv_projection
+from kernelforge_amd.SANA_LinearAttention import (CUDAGraphJointLiteLA, CustomLiteLA, CustomOpJointLiteLA,
+                                                  GroupedFull64QOutLiteLA, JointLiteLA, LiteLA, apply_rotary_emb,
+                                                  optimized_joint_litela, qkv_projection)
 from oracle import rmsnorm as orms
 from oracle import sana as osana
 
@@ -172,3 +177,65 @@ def test_rms_norm_rows_rejects_uneven_rows():
     y = torch.randn(4, 6, 16, device=DEV)[:3, :5]  # row spacing jumps between dim 0 blocks
     with pytest.raises(ValueError):
         rms_norm_rows_(y, torch.ones(16, device=DEV))
+
+
+def _joint_pair(cls, B, N, C, qk_norm, seed=0):
+    torch.manual_seed(seed)
+    ref = JointLiteLA(C, C, batch=B, seq_len=N, dtype=torch.bfloat16, qk_norm=qk_norm).to(DEV, torch.bfloat16)
+    m = cls(C, C, batch=B, seq_len=N, dtype=torch.bfloat16, qk_norm=qk_norm).to(DEV, torch.bfloat16)
+    m.load_state_dict(ref.state_dict())
+    return ref, m
+
+
+@pytest.mark.parametrize("qk_norm", (False, True))
+def test_custom_op_joint_litela(qk_norm):
+    B, N, C = 2, 256, 8 * 32
+    ref, m = _joint_pair(CustomOpJointLiteLA, B, N, C, qk_norm)
+    x = torch.randn(B, N, C, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        want = ref(x)
+        got = m(x)
+        # Dynamo traces the module as one opaque operator (no graph break).
+        compiled = torch.compile(m, backend="aot_eager", fullgraph=True)(x)
+    assert torch.equal(got, want)
+    assert torch.equal(compiled, want)
+    _close(got, _module_ref(ref, x, qk_norm))
+    # rotary_emb takes the JointLiteLA path
+    rot = _rope_tables(N, 32)
+    with torch.inference_mode():
+        assert torch.equal(m(x, rotary_emb=rot), ref(x, rotary_emb=rot))
+    with pytest.raises(ValueError, match="expected LiteLA input shape"):
+        m(x[:, :-1])
+
+
+def test_cuda_graph_joint_litela():
+    B, N, C = 1, 512, 1152
+    ref, _ = _joint_pair(JointLiteLA, B, N, C, False)
+    g = CUDAGraphJointLiteLA(ref)
+    gen = torch.Generator().manual_seed(6)
+    xs = [torch.randn(B, N, C, generator=gen).to(torch.bfloat16).to(DEV) for _ in range(3)]
+    replays = []
+    for x in xs + xs[:1]:
+        out = g(x).clone()
+        torch.cuda.synchronize()
+        with torch.inference_mode():
+            eager = ref(x)  # eager work between replays
+        torch.cuda.synchronize()
+        _close(out, eager.cpu().float(), tol=1e-2)
+        replays.append(out)
+    # the same input replays to the same bits
+    assert torch.equal(replays[0], replays[3])
+    _close(replays[1], _module_ref(ref, xs[1], False))
+
+
+def test_grouped_full64_module_and_selector():
+    B, N, C = 1, 1024, 1152
+    m = optimized_joint_litela(C, C, batch=B, seq_len=N, dtype=torch.bfloat16, heads=36, dim=32)
+    assert type(m) is GroupedFull64QOutLiteLA
+    m = m.to(DEV, torch.bfloat16)
+    x = torch.randn(B, N, C, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).to(DEV)
+    with torch.inference_mode():
+        got = m(x)
+    _close(got, _module_ref(m, x, False))
+    with pytest.raises(ValueError, match="rotary_emb=None"):
+        m(x, rotary_emb=_rope_tables(N, 32))

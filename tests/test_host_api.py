@@ -87,3 +87,31 @@ def test_fake_impls_for_tracing():
         assert t.shape == q.shape
         dq, dk, dv = fa._bwd_fake(q, q, k, k, q, lse, 0.1, False)
         assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == k.shape
+
+
+def test_litela_variants_on_the_host():
+    """Module selection and constructor checks of the LiteLA variants
+    (SANA_LinearAttention/custom.py:812-868); the joint custom operator has a
+    fake implementation for tracing."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    from kernelforge_amd.SANA_LinearAttention import (CustomOpJointLiteLA, GroupedFull64QOutLiteLA, JointLiteLA,
+                                                      optimized_joint_litela)
+    from kernelforge_amd.SANA_LinearAttention import modules
+
+    kw = dict(batch=1, seq_len=1024, dtype=torch.bfloat16)
+    assert type(optimized_joint_litela(1152, 1152, heads=36, **kw)) is GroupedFull64QOutLiteLA
+    assert type(optimized_joint_litela(256, 256, batch=2, seq_len=64, dtype=torch.bfloat16)) is JointLiteLA
+    for bad in (dict(kw, batch=2), dict(kw, dtype=torch.float16), dict(kw, qk_norm=True),
+                dict(kw, use_bias=True), dict(kw, heads=18)):
+        with pytest.raises(ValueError, match="GroupedFull64QOutLiteLA requires"):
+            GroupedFull64QOutLiteLA(1152, 1152, **bad)
+    m = CustomOpJointLiteLA(256, 256, batch=2, seq_len=64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="device"):
+        m(torch.zeros(2, 64, 256, dtype=torch.bfloat16))
+    with FakeTensorMode():
+        x = torch.empty(2, 64, 256, dtype=torch.bfloat16)
+        w = torch.empty(768, 256, dtype=torch.bfloat16)
+        pw = torch.empty(256, 256, dtype=torch.bfloat16)
+        y = modules._joint_litela_op_fake(x, w, None, pw, None, None, None, 8, 32, 1e-15, 1e-5)
+        assert y.shape == (2, 64, 256) and y.dtype == torch.bfloat16
