@@ -13,13 +13,20 @@ Timing: inputs are resident in HBM before the timed region; input/output
 sets rotate so that the bytes touched between two uses of a buffer exceed
 the 256 MB Infinity Cache; the timed region is bracketed by
 torch.cuda.synchronize() and measured with HIP events recorded on the
-stream the kernels are launched on (torch's current stream).
+stream the kernels are launched on (torch's current stream).  Warm-up: the W
+untimed launches, then more untimed launches until 100 ms of the workload
+have run on the GPU, because the clocks keep ramping for tens of
+milliseconds after an idle period (measured on MI355X: the first 9 ms after
+a 10-launch warm-up ran 4-6% slower than the steady state, the first ~90 ms
+of the fused FA kernel 7% slower; the rate after that stayed within 0.3%
+over two seconds of back-to-back launches).  The reported
+"warmup" is the number of untimed launches of the headline workload.
 
 The CPU baseline times the oracle (a plain-torch restatement of the
 reference original.py, test infrastructure) on the host cores on a bounded
 sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu] [--settle-ms MS]
 """
 
 from __future__ import annotations
@@ -47,18 +54,36 @@ def _sets_for(bytes_per_set: int) -> int:
     return max(2, min(16, -(-2 * MALL_BYTES // max(1, bytes_per_set)) + 1))
 
 
-def _time_launches(fn, n_sets: int, steps: int, warmup: int) -> float:
-    """Average microseconds per launch of fn(set_index) over `steps` launches."""
-    for i in range(warmup):
-        fn(i % n_sets)
-    torch.cuda.synchronize()
+SETTLE_MS = 100.0
+
+
+def _time_launches(fn, n_sets: int, steps: int, warmup: int) -> tuple[float, int]:
+    """(average microseconds per launch of fn(set_index) over `steps` launches,
+    untimed launches before them): `warmup` launches, then batches of about
+    10 ms each until SETTLE_MS of GPU time has run."""
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_warm = 0
+    for _ in range(warmup):
+        fn(n_warm % n_sets)
+        n_warm += 1
+    torch.cuda.synchronize()
+    settled, batch = 0.0, 1
+    while settled < SETTLE_MS:
+        start.record()
+        for _ in range(batch):
+            fn(n_warm % n_sets)
+            n_warm += 1
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end)
+        settled += ms
+        batch = max(1, min(4 * batch, int(batch * 10.0 / max(ms, 1e-3))))
     start.record()
     for i in range(steps):
         fn(i % n_sets)
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1000.0 / steps
+    return start.elapsed_time(end) * 1000.0 / steps, n_warm
 
 
 def _gen(seed):
@@ -88,9 +113,10 @@ def bench_rmsnorm(hidden: int, steps: int, warmup: int, rows: int = 16384) -> di
         if rc:
             _lib.check(rc, "kf_rmsnorm_fwd")
 
-    us = _time_launches(launch, n_sets, steps, warmup)
+    us, n_warm = _time_launches(launch, n_sets, steps, warmup)
     gbs = bytes_per_launch / (us * 1e-6) / 1e9
     return dict(kernel="rmsnorm_vec_kernel", workload=f"rmsnorm_bf16_{rows}x{hidden}", us=us,
+                warmup_launches=n_warm, steps=steps,
                 bytes=bytes_per_launch, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, sets=n_sets)
 
 
@@ -119,10 +145,11 @@ def bench_sana(B: int, H: int, N: int, steps: int, warmup: int, D: int = 32) -> 
         if rc:
             _lib.check(rc, "kf_linattn_fwd")
 
-    us = _time_launches(launch, n_sets, steps, warmup)
+    us, n_warm = _time_launches(launch, n_sets, steps, warmup)
     gbs = bytes_per_launch / (us * 1e-6) / 1e9
     tflops = flops / (us * 1e-6) / 1e12
     return dict(kernel="linattn (state+reduce+out)", workload=f"sana_bf16_B{B}_H{H}_D{D}_N{N}", us=us,
+                warmup_launches=n_warm, steps=steps,
                 bytes=bytes_per_launch, flops=flops, gbs=gbs, tflops=tflops,
                 roofline_frac=gbs / HBM_PEAK_GBS, mfma_frac=tflops / BF16_PEAK_TFLOPS, splits=splits,
                 sets=n_sets)
@@ -173,10 +200,11 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
         if rc:
             _lib.check(rc, name)
 
-    us = _time_launches(launch, 1, steps, warmup)
+    us, n_warm = _time_launches(launch, 1, steps, warmup)
     flops = 2 * gemms * B * H * N * N * D
     tflops = flops / (us * 1e-6) / 1e12
     return dict(kernel=name, workload=f"fa_{mode}_bf16_B{B}_H{H}_N{N}_D{D}", us=us, flops=flops,
+                warmup_launches=n_warm, steps=steps,
                 gemm_equivalents=gemms, tflops=tflops, roofline_frac=tflops / BF16_PEAK_TFLOPS)
 
 
@@ -186,8 +214,9 @@ def bench_copy(steps: int, warmup: int) -> dict:
     n_sets = 4
     src = [torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_() for _ in range(n_sets)]
     dst = [torch.empty_like(s) for s in src]
-    us = _time_launches(lambda i: dst[i].copy_(src[i]), n_sets, steps, warmup)
+    us, n_warm = _time_launches(lambda i: dst[i].copy_(src[i]), n_sets, steps, warmup)
     return dict(kernel="torch copy_", workload="copy_bf16_256MiB", bytes=4 * n, us=us,
+                warmup_launches=n_warm, steps=steps,
                 gbs=4 * n / (us * 1e-6) / 1e9)
 
 
@@ -250,6 +279,7 @@ def load_traffic() -> dict:
 
 
 def main() -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -258,7 +288,10 @@ def main() -> int:
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
                          "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|copy), e.g. under rocprofv3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="GPU time of untimed launches after the warm-up steps (clock settling)")
     args = ap.parse_args()
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; run with --gpus 1 (the hot paths are "
               "single-GPU kernels; sharding is described in DESIGN.md)", file=sys.stderr)
@@ -309,8 +342,8 @@ def main() -> int:
         "value": round(head["gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
+        "steps": head["steps"],
+        "warmup": head["warmup_launches"],
         "ms_per_step": head["us"] / 1000.0,
         "higher_is_better": True,
         "scaling": "weak",

@@ -13,7 +13,10 @@
 // A row is owned by WPR waves (WPR = 1 needs no LDS and no barrier).  Rows of
 // 4-16 KiB are spread over 2-8 waves with 2 vectors per lane: short-lived
 // waves with few loads each kept the HBM queues fuller than long-lived ones
-// in sweeps of (VPT, WPR, block size) on MI355X.
+// in sweeps of (VPT, WPR, block size) on MI355X.  Blocks holding two rows
+// stage the weight in LDS once per block: re-reading it from L2 for every row
+// cost 2-3% of the HBM rate at 2048-4096 channels; with one row per block
+// (8192) the staging costs more than it saves.
 #include "kf_common.h"
 
 namespace kf {
@@ -39,6 +42,12 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, con
     const bool row_ok = row < rows;
     const int nvec = dim / VEC;
 
+    // Blocks of two or more rows read the weight once per block into LDS
+    // instead of once per row (an 8 KiB L2 read per row at dim 4096).
+    constexpr bool kStageW = HAS_W && WPR > 1 && ROWS_PER_BLOCK > 1;
+    __shared__ u32x4 wl[kStageW ? VPT * WPR * 64 : 1];
+    const u32x4* wr = reinterpret_cast<const u32x4*>(w);
+
     const u32x4* xr = reinterpret_cast<const u32x4*>(x + row * ld_x);
     u32x4 xv[VPT];
     float ss = 0.f;
@@ -50,6 +59,12 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, con
         } else {
             xv[i] = u32x4{0u, 0u, 0u, 0u};
         }
+    }
+    if constexpr (kStageW) {
+        for (int j = threadIdx.x; j < nvec; j += 64 * WAVES) wl[j] = wr[j];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
         const T* e = reinterpret_cast<const T*>(&xv[i]);
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
@@ -61,7 +76,7 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, con
     if constexpr (WPR > 1) {
         __shared__ float part[WAVES];
         if (lane == 0) part[wave] = ss;
-        __syncthreads();
+        __syncthreads();  // also publishes the staged weight
         float t = 0.f;
 #pragma unroll
         for (int s = 0; s < WPR; ++s) t += part[row_in_block * WPR + s];
@@ -70,7 +85,6 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, con
     if (!row_ok) return;
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
 
-    const u32x4* wr = reinterpret_cast<const u32x4*>(w);
     u32x4* yr = reinterpret_cast<u32x4*>(y + row * ld_y);
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -78,7 +92,10 @@ __global__ __launch_bounds__(64 * WAVES) void rmsnorm_vec_kernel(const T* x, con
         if (j < nvec) {
             const T* e = reinterpret_cast<const T*>(&xv[i]);
             u32x4 wv;
-            if constexpr (HAS_W) wv = wr[j];
+            if constexpr (kStageW)
+                wv = wl[j];
+            else if constexpr (HAS_W)
+                wv = wr[j];
             const T* we = reinterpret_cast<const T*>(&wv);
             u32x4 ov;
             T* o = reinterpret_cast<T*>(&ov);
