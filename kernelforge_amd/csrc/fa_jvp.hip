@@ -166,10 +166,13 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     for (int rb = 0; rb < R; ++rb) klim[rb] = p.causal ? min(p.Nk - 1, qr[rb] + diag) : p.Nk - 1;
     const float c = p.scale_log2;
 
-    // Row statistics (each lane holds a quarter of its row's keys).  l_run and
-    // r_run sum the 16-bit E and H values the products consume, so O is an
-    // exact convex combination of V rows and tO = sum_j H_j (v_j - O) / l;
-    // l_lse sums the fp32 E for the LSE output.  m_run is in log2 units.
+    // Row statistics (each lane holds a quarter of its row's keys).  In the
+    // JVP modes l_run and r_run sum the 16-bit E and H values the products
+    // consume, so O is an exact convex combination of V rows and
+    // tO = sum_j H_j (v_j - O) / l.  l_lse sums the fp32 E for the LSE output;
+    // the forward alone also normalises O by it (as flash-attn does), which
+    // saves a dot product per pair of keys in its VALU-bound inner loop.
+    // m_run is in log2 units.
     float m_run[R], l_run[R], r_run[R], l_lse[R];
     // Exponent offset: -m_run, or -LSE (log2 units) in the JVP mode (+inf LSE
     // -> P = 0).
@@ -301,7 +304,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
                 if constexpr (MODE != FA_JVP) esum += e0 + e1;
                 const unsigned pe = Pk<T>::cvt(e0, e1);
                 ew[i2][j] = pe;
-                l_run[rb] = Pk<T>::sum_into(pe, l_run[rb]);
+                if constexpr (JVP) l_run[rb] = Pk<T>::sum_into(pe, l_run[rb]);
                 if constexpr (JVP) {
                     const unsigned ph = Pk<T>::cvt(e0 * (ts[i2][2 * j] * p.scale), e1 * (ts[i2][2 * j + 1] * p.scale));
                     hw[i2][j] = ph;
@@ -439,7 +442,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
 #pragma unroll
     for (int rb = 0; rb < R; ++rb) {
-        const float l_tot = row_sum4(l_run[rb]);
+        const float l_tot = JVP ? row_sum4(l_run[rb]) : row_sum4(l_lse[rb]);
         const float r_tot = row_sum4(r_run[rb]);
         const float l_lse_tot = row_sum4(l_lse[rb]);
         T* orow = static_cast<T*>(p.o) + q_off[rb];
