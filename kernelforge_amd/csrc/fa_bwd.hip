@@ -421,24 +421,34 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
 #pragma unroll
             for (int db = 0; db < PF && db < DB; ++db) t_load(db);
             u32x2 pw[2], sw[2];
+            // P and dS; the causal test runs only on tiles that cross the
+            // diagonal (a uniform branch, so unmasked tiles pay nothing).
+            auto probs = [&](auto mkc) {
 #pragma unroll
-            for (int i2 = 0; i2 < 2; ++i2) {
-                const int rl = 16 * (2 * h + i2) + 4 * grp;
-                const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
-                const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + rl);
-                float pr[4], dsv[4];
+                for (int i2 = 0; i2 < 2; ++i2) {
+                    const int rl = 16 * (2 * h + i2) + 4 * grp;
+                    const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
+                    const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + rl);
+                    float pr[4], dsv[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float e = fast_exp2(fmaf(s[i2][i], c, -l2[i]));
-                    if (masked && kr > r0 + rl + i + diag) e = 0.f;
-                    pr[i] = e;
-                    dsv[i] = e * (dp[i2][i] - dl[i]);
+                    for (int i = 0; i < 4; ++i) {
+                        float e = fast_exp2(fmaf(s[i2][i], c, -l2[i]));
+                        if constexpr (decltype(mkc)::value) {
+                            if (kr > r0 + rl + i + diag) e = 0.f;
+                        }
+                        pr[i] = e;
+                        dsv[i] = e * (dp[i2][i] - dl[i]);
+                    }
+                    pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
+                    pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
+                    sw[i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
+                    sw[i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
                 }
-                pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
-                pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
-                sw[i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
-                sw[i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
-            }
+            };
+            if (masked)
+                probs(std::true_type{});
+            else
+                probs(std::false_type{});
             const x8 pb = __builtin_bit_cast(x8, u32x4{pw[0][0], pw[0][1], pw[1][0], pw[1][1]});
             const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
 #pragma unroll
