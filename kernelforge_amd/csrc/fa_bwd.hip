@@ -190,10 +190,11 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
                 kring[st % NR] = row_chunk<T, DP>(Kt, krow, 4 * (st % DS) + grp);
                 vring[st % NR] = row_chunk<T, DP>(Vt, krow, 4 * (st % DS) + grp);
             };
+            // dP^T accumulates onto -Delta, so it ends as dP - Delta.
 #pragma unroll
             for (int i2 = 0; i2 < 2; ++i2) {
                 s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dp[i2] = f32x4{-delta, -delta, -delta, -delta};
             }
 #pragma unroll
             for (int st = 0; st < PF && st < NSTEP; ++st) kv_load(st);
@@ -226,7 +227,7 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
                 for (int j = 0; j < 2; ++j) {
                     const float p0 = fast_exp2(fmaf(s[i2][2 * j], c, nlse2));
                     const float p1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nlse2));
-                    sw[i2][j] = Pk<T>::cvt(p0 * (dp[i2][2 * j] - delta), p1 * (dp[i2][2 * j + 1] - delta));
+                    sw[i2][j] = Pk<T>::cvt(p0 * dp[i2][2 * j], p1 * dp[i2][2 * j + 1]);
                 }
             const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
 #pragma unroll
@@ -397,10 +398,12 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
                 qring[st % NR] = row_chunk<T, DP>(Qt, row, 4 * (st % DS) + grp);
                 oring[st % NR] = row_chunk<T, DP>(Ot, row, 4 * (st % DS) + grp);
             };
+            // dP accumulates onto -Delta of its rows, so it ends as dP - Delta.
 #pragma unroll
             for (int i2 = 0; i2 < 2; ++i2) {
+                const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + 16 * (2 * h + i2) + 4 * grp);
                 s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                dp[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                dp[i2] = -dl;
             }
 #pragma unroll
             for (int st = 0; st < PF && st < NSTEP; ++st) qo_load(st);
@@ -428,7 +431,6 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
                 for (int i2 = 0; i2 < 2; ++i2) {
                     const int rl = 16 * (2 * h + i2) + 4 * grp;
                     const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
-                    const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + rl);
                     float pr[4], dsv[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -437,7 +439,7 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
                             if (kr > r0 + rl + i + diag) e = 0.f;
                         }
                         pr[i] = e;
-                        dsv[i] = e * (dp[i2][i] - dl[i]);
+                        dsv[i] = e * dp[i2][i];
                     }
                     pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
                     pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
