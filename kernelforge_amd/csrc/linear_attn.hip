@@ -14,8 +14,8 @@
 //      V per token) through LDS and accumulates S with v_mfma_f32_32x32x16; the
 //      token-major operands are read with ds_read_b64_tr_b16.  z accumulates on
 //      the VALU from the same registers.  Partials [B][H][splits][D+1][D] fp32.
-//   2. linattn_reduce_kernel  one thread per state element: sums the partials in
-//      split order (fixed order: deterministic, no atomics).
+//   2. linattn_reduce_kernel  four state elements per thread: sums the partials
+//      in split order (fixed order: deterministic, no atomics).
 //   3. linattn_out_kernel     grid (ceil(H/4), ceil(N/64), B): one wavefront per
 //      head keeps S and z in registers as hi+lo 16-bit pairs (so the products
 //      carry ~16 mantissa bits of the fp32 state); relu(q) of 64 tokens x 4
@@ -192,29 +192,47 @@ __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict_
 // --------------------------------------------------------------------------
 // 2. Fixed-order reduction of the split partials.
 // --------------------------------------------------------------------------
-// One thread per state element of one (batch, head); the partials of all
-// splits are loaded eight at a time before they are added, in split order
-// (deterministic, no atomics).
+// VEC consecutive state elements of one (batch, head) per thread; the
+// partials of all splits are loaded eight at a time (a short last batch is
+// padded with zeros, so every batch is one round of independent loads) and
+// added in split order (deterministic, no atomics).
+template <int VEC>
 __global__ __launch_bounds__(256) void linattn_reduce_kernel(const float* __restrict__ partial,
                                                              float* __restrict__ state,
                                                              int64_t n_heads, int splits,
                                                              int state_size) {
-    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    typedef float fv __attribute__((ext_vector_type(VEC)));
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
     if (idx >= n_heads * state_size) return;
     const int64_t bh = idx / state_size;
-    const int e = (int)(idx - bh * state_size);
+    const int e = (int)(idx - bh * state_size);  // state_size % VEC == 0: one (b, h)
     const float* P = partial + bh * splits * (int64_t)state_size + e;
-    float acc = 0.f;
-    int s = 0;
-    for (; s + 8 <= splits; s += 8) {
-        float v[8];
+    fv acc = {};
+    for (int s = 0; s < splits; s += 8) {
+        fv v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = P[(int64_t)(s + j) * state_size];
+        for (int j = 0; j < 8; ++j)
+            v[j] = s + j < splits ? *reinterpret_cast<const fv*>(P + (int64_t)(s + j) * state_size) : fv{};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += v[j];
+        for (int j = 0; j < 8; ++j) acc += v[j];  // a padded zero leaves acc unchanged
     }
-    for (; s < splits; ++s) acc += P[(int64_t)s * state_size];
-    state[idx] = acc;
+    *reinterpret_cast<fv*>(state + idx) = acc;
+}
+
+// Launch of the reduction: four elements per thread when a state is a whole
+// number of 16-byte vectors (all head dims but 1 and 2) and the workspace is
+// 16-byte aligned.
+int launch_reduce(const float* partial, float* state, int64_t n_heads, int splits, int state_size,
+                  hipStream_t stream) {
+    const int64_t n = n_heads * state_size;
+    if (state_size % 4 == 0 && (uintptr_t)partial % 16 == 0) {
+        hipLaunchKernelGGL(linattn_reduce_kernel<4>, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0,
+                           stream, partial, state, n_heads, splits, state_size);
+    } else {
+        hipLaunchKernelGGL(linattn_reduce_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           stream, partial, state, n_heads, splits, state_size);
+    }
+    return check_launch("linattn_reduce_kernel launch");
 }
 
 // --------------------------------------------------------------------------
@@ -493,10 +511,7 @@ int run_mfma(const void* qkv, void* out, float* partial, float* state, int B, in
     hipLaunchKernelGGL((linattn_state_kernel<T>), dim3((H + 1) / 2, splits, B), dim3(256), 0,
                        stream, static_cast<const T*>(qkv), partial, N, H, split_len, splits);
     if (int rc = check_launch("linattn_state_kernel launch")) return rc;
-    const int64_t n_state = (int64_t)B * H * (kState);
-    hipLaunchKernelGGL(linattn_reduce_kernel, dim3((unsigned)((n_state + 255) / 256)), dim3(256), 0,
-                       stream, partial, state, (int64_t)B * H, splits, kState);
-    if (int rc = check_launch("linattn_reduce_kernel launch")) return rc;
+    if (int rc = launch_reduce(partial, state, (int64_t)B * H, splits, kState, stream)) return rc;
     hipLaunchKernelGGL((linattn_out_kernel<T, TO>),
                        dim3((H + 3) / 4, out_grid_y(N), B), dim3(256), 0,
                        stream, static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);
@@ -509,10 +524,7 @@ int run_generic(const void* qkv, void* out, float* partial, float* state, int B,
     hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(H, splits, B), dim3(256), 0, stream,
                        static_cast<const T*>(qkv), partial, N, H, split_len, splits);
     if (int rc = check_launch("linattn_state_generic launch")) return rc;
-    const int64_t n_state = (int64_t)B * H * ((DG + 1) * DG);
-    hipLaunchKernelGGL(linattn_reduce_kernel, dim3((unsigned)((n_state + 255) / 256)), dim3(256), 0,
-                       stream, partial, state, (int64_t)B * H, splits, (DG + 1) * DG);
-    if (int rc = check_launch("linattn_reduce_kernel launch")) return rc;
+    if (int rc = launch_reduce(partial, state, (int64_t)B * H, splits, (DG + 1) * DG, stream)) return rc;
     hipLaunchKernelGGL((linattn_out_generic<T, TO, DG>),
                        dim3(H, out_grid_y(N), B), dim3(256), 0, stream,
                        static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);

@@ -7,6 +7,8 @@ checks the relative Frobenius error, which a dropped term or a wrong index
 would fail.
 """
 
+import ctypes
+
 import pytest
 import torch
 
@@ -52,7 +54,7 @@ def test_ragged_shapes(B, H, N, dtype):
     check(out, orc.linear_attention(qkv, H, 32), 1e-4)
 
 
-@pytest.mark.parametrize("splits", [1, 2, 7, 64])
+@pytest.mark.parametrize("splits", [1, 2, 7, 13, 64])
 def test_split_invariance(splits):
     """The split count changes only the fp32 summation order."""
     qkv = randn((1, 4096, 3, 8 * 32), torch.bfloat16, seed=11).to(DEV)
@@ -113,3 +115,26 @@ def test_validation_and_splits():
     with pytest.raises(ValueError):
         run(torch.zeros(1, 17, 3, 64, device=DEV, dtype=torch.bfloat16))
     assert default_splits(2, 70, 32, 4096) >= 1
+
+
+@pytest.mark.parametrize("dim", [32, 16])
+def test_unaligned_workspace_matches_aligned(dim):
+    """The split reduction reads 16-byte vectors only from an aligned
+    workspace; a workspace 4 bytes off takes the scalar reduction, which sums
+    in the same split order and so gives the same bits."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    H, N, splits = 256 // dim, 1000, 13
+    qkv = randn((2, N, 3, H * dim), torch.bfloat16, seed=5).to(DEV)
+    need = int(lib.kf_linattn_workspace_bytes(2, H, dim, splits))
+    ws = torch.empty(need + 64, device=DEV, dtype=torch.uint8)
+    outs = []
+    for off in (0, 4):
+        out = torch.empty(2, N, H * dim, device=DEV, dtype=torch.float32)
+        rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), ctypes.c_void_p(ws.data_ptr() + off), need, 2, N, H,
+                                dim, splits, 1e-15, _lib.KF_BF16, _lib.KF_F32, _lib.stream_of(qkv))
+        _lib.check(rc, "kf_linattn_fwd")
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1])
+    check(outs[0], orc.linear_attention(qkv.cpu(), H, dim), 1e-4)
