@@ -19,8 +19,9 @@ have run on the GPU, because the clocks keep ramping for tens of
 milliseconds after an idle period (measured on MI355X: the first 9 ms after
 a 10-launch warm-up ran 4-6% slower than the steady state, the first ~90 ms
 of the fused FA kernel 7% slower; the rate after that stayed within 0.3%
-over two seconds of back-to-back launches).  The reported
-"warmup" is the number of untimed launches of the headline workload.
+over two seconds of back-to-back launches).  The line reports the requested
+W as "warmup", and the headline's untimed launches in total (W plus the
+settling ones) as "warmup_launches".
 
 The CPU baseline times the oracle (a plain-torch restatement of the
 reference original.py, test infrastructure) on the host cores on a bounded
@@ -343,7 +344,9 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": head["steps"],
-        "warmup": head["warmup_launches"],
+        "warmup": warmup,
+        "warmup_launches": head["warmup_launches"],
+        "settle_ms": SETTLE_MS,
         "ms_per_step": head["us"] / 1000.0,
         "higher_is_better": True,
         "scaling": "weak",
