@@ -295,7 +295,7 @@ def main() -> int:
     SETTLE_MS = args.settle_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; run with --gpus 1 (the hot paths are "
-              "single-GPU kernels; sharding is described in DESIGN.md)", file=sys.stderr)
+              "single-GPU kernels; no run here uses a second GPU)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
