@@ -172,12 +172,16 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
     dims = (B, N, N, H, H, D, scale, 0, _lib.KF_BF16, stream)
     if mode == "fwd_jvp":
         fnc, a = lib.kf_fa_fwd_jvp, (*P, *dims)
-        gemms, name = 6, "fa_kernel<bf16,128,FWD_JVP>"
+        gemms, executed, name = 6, 6, "fa_kernel<bf16,128,FWD_JVP>"
     elif mode == "jvp":
+        # JVP from the cached LSE: the algorithmic count is 5 GEMM-equivalents
+        # (S, tq.k, q.tk, H.v, P.tv).  The kernel also recomputes U = P.v in
+        # fp32 instead of reading the 16-bit O (6 executed); that extra product
+        # is reported as executed work, not counted as throughput.
         rc = lib.kf_fa_fwd(P[0], P[1], P[2], P[6], P[7], *dims)
         _lib.check(rc, "kf_fa_fwd")
         fnc, a = lib.kf_fa_jvp, (*P, *dims)
-        gemms, name = 6, "fa_kernel<bf16,128,JVP>"
+        gemms, executed, name = 5, 6, "fa_kernel<bf16,128,JVP>"
     elif mode == "bwd":
         # Backward from the forward's O and LSE: dq kernel + dkdv kernel.  The
         # algorithmic count is the usual 5 GEMM-equivalents (S recomputed
@@ -191,10 +195,10 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
         fnc = lib.kf_fa_bwd
         a = (P[0], P[1], P[2], P[6], P[7], _lib.ptr(dout), *(_lib.ptr(x) for x in grads), _lib.ptr(ws),
              ws_bytes, *dims)
-        gemms, name = 5, "fa_bwd_dq_kernel+fa_bwd_dkdv_kernel<bf16,128>"
+        gemms, executed, name = 5, 7, "fa_bwd_dq_kernel+fa_bwd_dkdv_kernel<bf16,128>"
     else:
         fnc, a = lib.kf_fa_fwd, (P[0], P[1], P[2], P[6], P[7], *dims)
-        gemms, name = 2, "fa_kernel<bf16,128,FWD>"
+        gemms, executed, name = 2, 2, "fa_kernel<bf16,128,FWD>"
 
     def launch(_):
         rc = fnc(*a)
@@ -206,19 +210,66 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
     tflops = flops / (us * 1e-6) / 1e12
     return dict(kernel=name, workload=f"fa_{mode}_bf16_B{B}_H{H}_N{N}_D{D}", us=us, flops=flops,
                 warmup_launches=n_warm, steps=steps,
-                gemm_equivalents=gemms, tflops=tflops, roofline_frac=tflops / BF16_PEAK_TFLOPS)
+                gemm_equivalents=gemms, executed_gemm_equivalents=executed,
+                executed_tflops=tflops * executed / gemms, tflops=tflops,
+                roofline_frac=tflops / BF16_PEAK_TFLOPS)
 
 
-def bench_copy(steps: int, warmup: int) -> dict:
-    """Device-to-device copy of 256 MiB: the achievable HBM stream ceiling."""
-    n = 128 * 2**20  # bf16 elements = 256 MiB
-    n_sets = 4
-    src = [torch.empty(n, device="cuda", dtype=torch.bfloat16).normal_() for _ in range(n_sets)]
-    dst = [torch.empty_like(s) for s in src]
-    us, n_warm = _time_launches(lambda i: dst[i].copy_(src[i]), n_sets, steps, warmup)
-    return dict(kernel="torch copy_", workload="copy_bf16_256MiB", bytes=4 * n, us=us,
-                warmup_launches=n_warm, steps=steps,
-                gbs=4 * n / (us * 1e-6) / 1e9)
+def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
+    """HBM stream ceiling: the library's 16-byte-per-lane copy kernel (kfm_copy,
+    kernelforge_amd/csrc/measure.hip) reading and writing `nbytes` each, the
+    traffic of one RMSNorm launch; the best of 1, 2 and 4 vectors per lane."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    n_sets = _sets_for(2 * nbytes)
+    src = [torch.empty(nbytes // 2, device="cuda", dtype=torch.bfloat16).normal_() for _ in range(n_sets)]
+    dst = [torch.empty_like(x) for x in src]
+    stream = _lib.stream_of(src[0])
+    ptrs = [(_lib.ptr(src[i]), _lib.ptr(dst[i])) for i in range(n_sets)]
+    best = None
+    for vpt in (1, 2, 4):
+        def launch(i, vpt=vpt):
+            rc = lib.kfm_copy(ptrs[i][0], ptrs[i][1], nbytes, vpt, stream)
+            if rc:
+                _lib.check(rc, "kfm_copy")
+
+        us, n_warm = _time_launches(launch, n_sets, steps, warmup)
+        if best is None or us < best["us"]:
+            best = dict(kernel="copy_kernel", workload=f"copy_{nbytes >> 20}MiB", vectors_per_lane=vpt,
+                        bytes=2 * nbytes, us=us, warmup_launches=n_warm, steps=steps)
+    best["gbs"] = best["bytes"] / (best["us"] * 1e-6) / 1e9
+    best["frac_of_peak"] = best["gbs"] / HBM_PEAK_GBS
+    return best
+
+
+def bench_mfma(warmup: int) -> dict:
+    """Dense bf16 MFMA ceiling: kfm_mfma_bf16 (four independent
+    v_mfma_f32_16x16x32_bf16 chains per wavefront) at 1, 2 and 4 wavefronts
+    per SIMD, each run ~2 ms; the best rate."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 8192
+    best = None
+    for waves_per_simd in (1, 2, 4):
+        blocks = cus * waves_per_simd  # 4 wavefronts (one per SIMD) per block
+        out = torch.empty(blocks * 256, device="cuda", dtype=torch.float32)
+        stream = _lib.stream_of(out)
+
+        def launch(_):
+            rc = lib.kfm_mfma_bf16(_lib.ptr(out), blocks, iters, stream)
+            if rc:
+                _lib.check(rc, "kfm_mfma_bf16")
+
+        us, _ = _time_launches(launch, 1, 5, warmup)
+        flops = blocks * 4 * iters * 4 * 16384
+        tflops = flops / (us * 1e-6) / 1e12
+        if best is None or tflops > best["tflops"]:
+            best = dict(kernel="mfma_kernel", workload="mfma_bf16_16x16x32_dense", waves_per_simd=waves_per_simd,
+                        us=us, flops=flops, tflops=tflops, frac_of_peak=tflops / BF16_PEAK_TFLOPS)
+    return best
 
 
 # ---------------------------------------------------------------------------
@@ -251,10 +302,17 @@ def cpu_baselines(rows=16384, hidden=4096) -> dict:
                           kind="port", seconds_per_pass=t,
                           sample=f"oracle.rmsnorm on the full bf16 [{rows},{hidden}] input, median of 5")
     qkv = torch.randn(2, 4096, 3, 70 * 32, generator=g).to(torch.bfloat16)
+    sana_flops = 4 * 2 * 70 * 4096 * 32 * 33
     t = med(lambda: osana.linear_attention(qkv, 70, 32), 3)
-    out["sana"] = dict(value=4 * 2 * 70 * 4096 * 32 * 33 / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+    out["sana"] = dict(value=sana_flops / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
                        seconds_per_pass=t,
-                       sample="oracle.sana.linear_attention (fp32) on the full B=2,H=70,N=4096 input, median of 3")
+                       sample="oracle.sana.linear_attention (fp32_attention=True) on the full B=2,H=70,N=4096 "
+                              "input, median of 3")
+    t = med(lambda: osana.linear_attention(qkv, 70, 32, fp32_attention=False), 3)
+    out["sana_eager_bf16"] = dict(value=sana_flops / t / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                                  seconds_per_pass=t,
+                                  sample="oracle.sana.linear_attention as written with bf16 matmuls "
+                                         "(fp32_attention=False) on the full B=2,H=70,N=4096 input, median of 3")
     # FA: one (batch, head) slice of B=2, H=16, N=4096, D=128 (1/32 of the work).
     q, k, v, tq, tk, tv = (torch.randn(1, 4096, 1, 128, generator=g).to(torch.bfloat16) for _ in range(6))
     t = med(lambda: ofa.attention_jvp(q, k, v, tq, tk, tv), 1)
@@ -263,7 +321,19 @@ def cpu_baselines(rows=16384, hidden=4096) -> dict:
                      seconds_full_config_est=32 * t,
                      sample="oracle.fa.attention_jvp (dense fp32 torch.func.jvp) on 1 of the 32 (b,h) "
                             "slices of B=2,H=16,N=4096,D=128, median of 1 after 1 warm-up")
+    out["cpu_model"] = cpu_model()
     return out
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (as lscpu prints it), from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def load_traffic() -> dict:
@@ -287,7 +357,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
-                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|copy), e.g. under rocprofv3")
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|copy2048|copy4096|copy8192|mfma), e.g. under rocprofv3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="GPU time of untimed launches after the warm-up steps (clock settling)")
@@ -313,7 +383,10 @@ def main() -> int:
         "fa_jvp": lambda: bench_fa("jvp", max(10, steps // 5), max(3, warmup // 2)),
         "fa_fwd": lambda: bench_fa("fwd", max(10, steps // 5), max(3, warmup // 2)),
         "fa_bwd": lambda: bench_fa("bwd", max(10, steps // 5), max(3, warmup // 2)),
-        "copy": lambda: bench_copy(max(5, steps // 5), 3),
+        "copy2048": lambda: bench_copy(16384 * 2048 * 2, steps, warmup),
+        "copy4096": lambda: bench_copy(16384 * 4096 * 2, steps, warmup),
+        "copy8192": lambda: bench_copy(16384 * 8192 * 2, steps, warmup),
+        "mfma": lambda: bench_mfma(warmup),
     }
     if args.only:
         r = runners[args.only]()
@@ -329,15 +402,22 @@ def main() -> int:
     tr = traffic.get(head["kernel"] + ":" + head["workload"])
     cpu = None if args.no_cpu else cpu_baselines()
     for name in results:
-        if cpu and name.startswith("rmsnorm") and name == "rmsnorm4096":
+        if cpu and name == "rmsnorm4096":
             results[name]["speedup_vs_cpu"] = head["gbs"] / cpu["rmsnorm"]["value"]
-        if cpu and name.startswith("sana"):
-            results[name]["speedup_vs_cpu_sanaA_oracle"] = results[name]["tflops"] / cpu["sana"]["value"]
-        if cpu and name.startswith("fa_") and name != "fa_bwd":
+        if cpu and name == "sanaA":
+            results[name]["speedup_vs_cpu_oracle_fp32"] = results[name]["tflops"] / cpu["sana"]["value"]
+            results[name]["speedup_vs_cpu_eager_bf16"] = (results[name]["tflops"]
+                                                          / cpu["sana_eager_bf16"]["value"])
+        if cpu and name == "fa_fwd_jvp":
             results[name]["speedup_vs_cpu"] = results[name]["tflops"] / cpu["fa"]["value"]
         t = traffic.get(results[name]["kernel"] + ":" + results[name]["workload"])
         if t is not None:
             results[name]["traffic_bytes"] = t
+        if name.startswith("rmsnorm"):
+            ceil = results["copy" + name[len("rmsnorm"):]]["gbs"]
+            results[name]["frac_of_copy_ceiling"] = results[name]["gbs"] / ceil
+        if name.startswith("fa_"):
+            results[name]["frac_of_mfma_ceiling"] = results[name]["tflops"] / results["mfma"]["tflops"]
     line = {
         "metric": BASELINE_METRIC,
         "value": round(head["gbs"], 2),
@@ -357,13 +437,15 @@ def main() -> int:
                    "input_sets_rotated": head["sets"]},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": tr,
-                     "algorithmic_bytes": head["bytes"], "kernel": head["kernel"]},
+                     "algorithmic_bytes": head["bytes"], "kernel": head["kernel"],
+                     "frac_of_copy_ceiling": round(head["frac_of_copy_ceiling"], 4)},
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["rmsnorm"]["value"], 3), "unit": "GB/s", "cores": cpu["rmsnorm"]["cores"],
             "kind": "port", "sample": cpu["rmsnorm"]["sample"]},
         "results": results,
         "cpu_baselines": cpu,
-        "copy_ceiling_gbs": round(results["copy"]["gbs"], 1),
+        "copy_ceiling_gbs": round(results["copy4096"]["gbs"], 1),
+        "mfma_ceiling_tflops": round(results["mfma"]["tflops"], 1),
     }
     print(json.dumps(line), flush=True)
     return 0

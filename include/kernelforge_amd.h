@@ -89,6 +89,38 @@ int kf_rmsnorm_fwd_strided(const void* x, const void* weight, void* y,
                            float eps, int dtype, kf_stream_t stream);
 
 /*
+ * kf_rmsnorm_fwd with torch's type promotion between x and the weight:
+ * y = y_dtype( float(x_dtype(x * inv)) * float(weight) ), where y_dtype must
+ * be promote(x_dtype, w_dtype) (equal types stay, any mix of fp32, fp16 and
+ * bf16 gives KF_F32).  Replaces RMSNorm.forward (rmsnorm/original.py:51-52)
+ * when the module's weight keeps its default fp32 dtype (original.py:25) and
+ * x is bf16 or fp16: `output * self.weight` then returns fp32.
+ * x: [rows, dim] of x_dtype; weight: [dim] of w_dtype; y: [rows, dim] of y_dtype.
+ */
+int kf_rmsnorm_fwd_mixed(const void* x, const void* weight, void* y,
+                         int64_t rows, int64_t dim, float eps,
+                         int x_dtype, int w_dtype, int y_dtype, kf_stream_t stream);
+
+/* Workspace bytes kf_rmsnorm_bwd needs (fp32 weight-gradient partials). */
+int64_t kf_rmsnorm_bwd_workspace_bytes(int64_t rows, int64_t dim);
+
+/*
+ * Gradients of kf_rmsnorm_fwd_mixed for the output gradient dy (of the
+ * promoted dtype), with the casts of RMSNorm.forward taken as identities,
+ * which is how torch's autograd differentiates rmsnorm/original.py:38, 51-52:
+ *   g  = float(x_dtype(dy * weight)),   n = x_dtype(x * inv),
+ *   dx = x_dtype(inv * g - x * inv^3 * sum(g * x) / dim),
+ *   dweight = w_dtype(sum over rows of dy * n)   (fp32 sum).
+ * dx: [rows, dim] of x_dtype; dweight: [dim] of w_dtype.  The weight
+ * gradient is summed over rows in a fixed order (deterministic, no atomics).
+ * workspace: at least kf_rmsnorm_bwd_workspace_bytes(rows, dim) bytes.
+ */
+int kf_rmsnorm_bwd(const void* x, const void* weight, const void* dy, void* dx,
+                   void* dweight, void* workspace, int64_t workspace_bytes,
+                   int64_t rows, int64_t dim, float eps, int x_dtype, int w_dtype,
+                   kf_stream_t stream);
+
+/*
  * Weight-free fp32 RMSNorm with the two-scan baseline's semantics:
  * b[r, :] = a[r, :] / sqrt(sum_c a[r, c]^2 / n + eps).
  *

@@ -23,6 +23,12 @@ Data path of ``forward(x[B, N, C])``:
    split reduction, MFMA output contraction), fp32 arithmetic.
 5. ``y = out @ Wproj^T + b`` -- library GEMM with the bias in its epilogue.
 
+Forward only: the linear-attention and rotary kernels have no backward, so
+``forward`` raises ``RuntimeError`` when autograd would need one (grad mode on
+and x or a parameter requiring grad); run the modules under
+``torch.inference_mode()`` or ``torch.no_grad()``, as the reference's tests do
+(SANA_LinearAttention/test.py:39, 73, 137).
+
 Numerics: the attention always runs with the reference's ``fp32_attention``
 semantics (ReLU on the stored 16-bit values, products and sums in fp32), so
 ``fp32_attention = True`` needs no separate path.  The reference sends
@@ -142,6 +148,16 @@ def _joint_litela_op_fake(x, qkv_weight, qkv_bias, proj_weight, proj_bias, q_nor
     return x.new_empty((*x.shape[:-1], proj_weight.shape[0]))
 
 
+def _require_inference(module: nn.Module, x: torch.Tensor) -> None:
+    """Refuse a forward whose result autograd would have to differentiate: the
+    attention kernels write through raw pointers and register no backward, so
+    gradients would silently stop at the output projection."""
+    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in module.parameters())):
+        raise RuntimeError(
+            f"{type(module).__name__} runs forward-only HIP kernels with no backward; call it under "
+            "torch.inference_mode() or torch.no_grad(), or freeze its parameters (requires_grad_(False))")
+
+
 class LiteLA(nn.Module):
     """Lightweight ReLU linear attention (SANA_LinearAttention/original.py:65-145).
 
@@ -212,6 +228,7 @@ class LiteLA(nn.Module):
         if x.dim() != 3 or x.shape[-1] != self.in_dim:
             raise ValueError(f"x must be [B, N, {self.in_dim}], got {tuple(x.shape)}")
         _lib.require_gpu(x)
+        _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         return self.proj(out)
 
@@ -241,6 +258,7 @@ class CustomLiteLA(LiteLA):
     def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
         self._validate_input(x)
         _lib.require_gpu(x)
+        _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         return self.proj(out)
 
@@ -261,6 +279,7 @@ class JointLiteLA(CustomLiteLA):
     def forward(self, x, mask=None, HW=None, rotary_emb=None, block_id=None, block_mask=None):
         self._validate_input(x)
         _lib.require_gpu(x)
+        _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
         return _project_out_joint(out, self.proj.weight, self.proj.bias)
 
@@ -277,6 +296,7 @@ class CustomOpJointLiteLA(JointLiteLA):
             return super().forward(x, mask, HW, rotary_emb, block_id, block_mask)
         self._validate_input(x)
         _lib.require_gpu(x)
+        _require_inference(self, x)
         qn, kn, norm_eps = self._norm_weights()
         return _joint_litela_op(x, self.qkv.weight, self.qkv.bias, self.proj.weight, self.proj.bias, qn, kn,
                                 self.heads, self.dim, self.eps, norm_eps)

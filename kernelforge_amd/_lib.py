@@ -35,6 +35,12 @@ SIGNATURES = {
     "kf_rmsnorm_fwd_strided": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p]),
     "kf_rmsnorm_noweight_f32": (_int, [_c_void_p, _c_void_p, _i64, _i64, _f32, _c_void_p]),
+    "kf_rmsnorm_fwd_mixed": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _int, _int, _int, _c_void_p]),
+    "kf_rmsnorm_bwd_workspace_bytes": (_i64, [_i64, _i64]),
+    "kf_rmsnorm_bwd": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _f32,
+               _int, _int, _c_void_p]),
     "kf_linattn_default_splits": (_i64, [_i64, _i64, _i64, _i64]),
     "kf_linattn_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "kf_linattn_fwd": (
@@ -69,6 +75,13 @@ SIGNATURES = {
     ),
 }
 
+# Measurement kernels (kernelforge_amd/csrc/measure.hip): exported by the
+# library for bench.py's ceilings, not part of the public header.
+MEASURE_SIGNATURES = {
+    "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _c_void_p]),
+    "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
+}
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
 
@@ -86,7 +99,7 @@ def load() -> ctypes.CDLL:
                     "build it with `python -m kernelforge_amd.build`"
                 )
             lib = ctypes.CDLL(str(LIB_PATH))
-            for name, (res, args) in SIGNATURES.items():
+            for name, (res, args) in {**SIGNATURES, **MEASURE_SIGNATURES}.items():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args

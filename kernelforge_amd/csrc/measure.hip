@@ -1,0 +1,93 @@
+// Measurement kernels: the attainable HBM stream rate and dense bf16 MFMA
+// rate of the device the library runs on.  bench.py reports them next to the
+// hot-path kernels as the ceilings those kernels are compared with.  They
+// compute nothing for a caller, so they are exported with the kfm_ prefix
+// and are not part of the public C ABI header.
+#include "kf_common.h"
+
+namespace kf {
+namespace {
+
+// Stream copy: thread t of block b moves the 16-byte vectors
+// (b * VPT + i) * 256 + t, i < VPT, so every load and store instruction of a
+// wavefront covers one contiguous 1 KiB span, the access shape of the
+// RMSNorm kernel.  All VPT loads are issued before the first store.
+template <int VPT>
+__global__ __launch_bounds__(256) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                   int64_t nvec) {
+    const int64_t base = (int64_t)blockIdx.x * 256 * VPT + threadIdx.x;
+    u32x4 v[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int64_t j = base + (int64_t)i * 256;
+        v[i] = j < nvec ? __builtin_nontemporal_load(src + j) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int64_t j = base + (int64_t)i * 256;
+        if (j < nvec) __builtin_nontemporal_store(v[i], dst + j);
+    }
+}
+
+// Dense bf16 MFMA issue rate: each wavefront runs `iters` rounds of four
+// independent v_mfma_f32_16x16x32_bf16 chains (16384 flops each), enough
+// independent accumulators to keep the pipe busy without register traffic.
+// The result is stored so the chains are not removed.
+__global__ __launch_bounds__(256) void mfma_kernel(float* __restrict__ out, int iters) {
+    V<bf16>::x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a[i] = (bf16)(threadIdx.x * 0.001f + i);
+        b[i] = (bf16)(i * 0.5f);
+    }
+    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0, c2 = c0, c3 = c0;
+    for (int it = 0; it < iters; ++it) {
+        c0 = mfma16x16x32(a, b, c0);
+        c1 = mfma16x16x32(a, b, c1);
+        c2 = mfma16x16x32(a, b, c2);
+        c3 = mfma16x16x32(a, b, c3);
+    }
+    const f32x4 s = c0 + c1 + c2 + c3;
+    out[(int64_t)blockIdx.x * 256 + threadIdx.x] = s[0] + s[1] + s[2] + s[3];
+}
+
+}  // namespace
+}  // namespace kf
+
+// Copy `bytes` (a multiple of 16, both pointers 16-byte aligned) from src to
+// dst with VPT = vectors_per_thread in {1, 2, 4, 8} 16-byte vectors per lane.
+extern "C" int kfm_copy(const void* src, void* dst, int64_t bytes, int vectors_per_thread,
+                        kf_stream_t stream) {
+    using namespace kf;
+    KF_REQUIRE(bytes >= 0 && bytes % 16 == 0, KF_E_INVALID, "copy: bytes %lld not a multiple of 16",
+               (long long)bytes);
+    KF_REQUIRE(bytes == 0 || (src && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0),
+               KF_E_INVALID, "copy: null or unaligned pointer");
+    if (bytes == 0) return KF_OK;
+    const int64_t nvec = bytes / 16;
+    const int vpt = vectors_per_thread;
+    const int64_t blocks = (nvec + 256LL * vpt - 1) / (256LL * vpt);
+    KF_REQUIRE(blocks <= 0x7fffffff, KF_E_UNSUPPORTED, "copy: too many blocks");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const u32x4* in = static_cast<const u32x4*>(src);
+    u32x4* o = static_cast<u32x4*>(dst);
+    switch (vpt) {
+        case 1: hipLaunchKernelGGL(copy_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, in, o, nvec); break;
+        case 2: hipLaunchKernelGGL(copy_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, in, o, nvec); break;
+        case 4: hipLaunchKernelGGL(copy_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, in, o, nvec); break;
+        case 8: hipLaunchKernelGGL(copy_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, in, o, nvec); break;
+        default: set_error("copy: vectors_per_thread must be 1, 2, 4 or 8, got %d", vpt); return KF_E_INVALID;
+    }
+    return check_launch("copy_kernel launch");
+}
+
+// Run the MFMA loop on `blocks` blocks of 256 threads for `iters` rounds;
+// out must hold blocks * 256 floats.  Flops = blocks * 4 * iters * 4 * 16384.
+extern "C" int kfm_mfma_bf16(float* out, int64_t blocks, int iters, kf_stream_t stream) {
+    using namespace kf;
+    KF_REQUIRE(out && blocks > 0 && blocks <= 0x7fffffff && iters > 0, KF_E_INVALID,
+               "mfma: bad arguments");
+    hipLaunchKernelGGL(mfma_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       out, iters);
+    return check_launch("mfma_kernel launch");
+}

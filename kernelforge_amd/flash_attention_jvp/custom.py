@@ -15,9 +15,11 @@ implement (flash-attention-jvp-derivation.md:388-558):
 - ``flash_attention_fwd_jvp(q, k, v, tq, tk, tv, *, softmax_scale, causal)``
   returning ``(out, lse, tangent)`` from one scan over the K/V tiles.
 
-Every operator is a ``torch.library.custom_op`` (namespace ``kernelforge_amd``)
-with a fake implementation, so torch.func transforms unwrap their tensors
-before the C ABI sees raw pointers and torch.compile can trace them.  Layouts
+Every operator is a ``torch.library.custom_op`` with a fake implementation,
+so torch.func transforms unwrap their tensors before the C ABI sees raw
+pointers and torch.compile can trace them.  The standalone JVP is the
+reference's ``kernelforge::flash_attention_jvp`` (same schema,
+custom.py:137-157); the others live in ``kernelforge_amd::``.  Layouts
 are ``[B, S, H, D]``; LSE is fp32 ``[B, Hq, Nq]`` in natural log.  Rows with no
 valid key (bottom-right causal masks with Nq > Nk) give out = 0, tangent = 0
 and LSE = +inf, the FlashAttention convention.
@@ -37,10 +39,22 @@ from torch.autograd.function import once_differentiable
 
 from .. import _lib
 
-# Schedule of the gfx950 kernel: 4 wavefronts x 32 query rows, 64-key tiles,
-# double-buffered LDS.  It is the same for every shape.
-_SCHEDULE = dict(block_m=128, block_n=64, threads=256, num_stages=2)
-_ALLOWED = dict(block_m=(16, 32, 64, 128), block_n=(32, 64, 128), threads=(128, 256), num_stages=(1, 2, 3))
+# Schedule values the reference accepts for explicit tile/pipeline arguments
+# (flash_attention_jvp/custom.py:214-217), plus the gfx950 JVP kernel's own
+# (_schedule below), so that ``flash_attention_jvp(..., **get_jvp_config(...))``
+# is accepted too.
+_ALLOWED = dict(block_m=(16, 32, 64, 128), block_n=(32, 64, 128), threads=(128, 256, 512),
+                num_stages=(1, 2, 3))
+
+
+def _schedule(head_dim: int) -> dict:
+    """Tile of the gfx950 JVP kernel for a head dim.  Head dims up to 128 run
+    128 query rows per workgroup (8 wavefronts x 16 rows, 512 threads) over
+    64-key tiles; 136-256 run 64 rows (4 wavefronts, 256 threads) over 32-key
+    tiles.  The K/V tiles are double-buffered in LDS in both (2 stages)."""
+    if head_dim > 128:
+        return dict(block_m=64, block_n=32, threads=256, num_stages=2)
+    return dict(block_m=128, block_n=64, threads=512, num_stages=2)
 
 
 def _validate_inputs(q, k, v, softmax_scale):
@@ -100,11 +114,18 @@ def _fwd_fake(q, k, v, scale, causal):
     return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[2], q.shape[1]), dtype=torch.float32)
 
 
-@torch.library.custom_op("kernelforge_amd::flash_attention_jvp", mutates_args=(), device_types="cuda")
-def _jvp_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Tensor | None,
-            tk: torch.Tensor | None, tv: torch.Tensor | None, out: torch.Tensor, lse: torch.Tensor,
-            scale: float, causal: bool) -> torch.Tensor:
+@torch.library.custom_op("kernelforge::flash_attention_jvp", mutates_args=(), device_types="cuda")
+def _launch_jvp(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Tensor, tk: torch.Tensor,
+                tv: torch.Tensor, out: torch.Tensor, lse: torch.Tensor, scale: float, causal: bool,
+                block_m: int, block_n: int, threads: int, num_stages: int) -> torch.Tensor:
+    """The reference's registered operator (flash_attention_jvp/custom.py:137-152),
+    same name and schema, on the gfx950 JVP kernel (kf_fa_jvp).  The schedule
+    arguments are accepted for schema compatibility; the kernel runs its own
+    tile for the head dim.  A tangent with no elements stands for a zero
+    tangent, whose products the kernel skips (the reference passes explicit
+    zeros, which give the same result)."""
     B, Nq, Nk, Hq, Hkv, D = _dims(q, k)
+    tq, tk, tv = (t if t.numel() else None for t in (tq, tk, tv))
     tout = torch.empty_like(out)
     rc = _lib.load().kf_fa_jvp(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(tq), _lib.ptr(tk),
                                _lib.ptr(tv), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(tout),
@@ -114,8 +135,8 @@ def _jvp_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Tensor 
     return tout
 
 
-@_jvp_op.register_fake
-def _jvp_fake(q, k, v, tq, tk, tv, out, lse, scale, causal):
+@_launch_jvp.register_fake
+def _launch_jvp_fake(q, k, v, tq, tk, tv, out, lse, scale, causal, block_m, block_n, threads, num_stages):
     return torch.empty_like(out)
 
 
@@ -184,13 +205,15 @@ def flash_attention_backward(dout, q, k, v, out, lse, *, softmax_scale=None, cau
 # Public API.
 # ---------------------------------------------------------------------------
 def get_jvp_config(q, k, v, *, softmax_scale=None, causal=False):
-    """Return the (fixed) schedule of the gfx950 JVP kernel without launching anything.
+    """Return the schedule of the gfx950 JVP kernel for these inputs without launching anything.
 
-    The reference returns its H20-tuned TileLang schedule (custom.py:123-134);
-    the gfx950 kernel has one schedule, reported here with the same keys.
+    Same keys as the reference (custom.py:123-134), which returns its
+    H20-tuned TileLang defaults; here the values are the tile the gfx950
+    kernel runs for the head dim (one schedule per head-dim class, the same
+    for causal and non-causal masks and every key length).
     """
     _validate_inputs(q, k, v, softmax_scale)
-    return dict(_SCHEDULE)
+    return _schedule(q.shape[-1])
 
 
 @torch.no_grad()
@@ -202,14 +225,17 @@ def flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, *, softmax_scale=None, ca
     lse: fp32 [B, Hq, Nq] in natural log, from the same primals, scale and mask.
     A ``None`` tangent denotes zero.  The result has q's dtype and out's shape.
     Schedule arguments are validated against the reference's accepted values
-    and otherwise do not change the computation (the kernel has one schedule).
+    (and the gfx950 kernel's own, as ``get_jvp_config`` reports them) and
+    otherwise do not change the computation: the kernel runs one tile per
+    head-dim class.  The launch goes through the registered operator
+    ``torch.ops.kernelforge.flash_attention_jvp`` (the reference's schema).
     """
     scale = _validate_inputs(q, k, v, softmax_scale)
     if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
         raise ValueError("out must have q's shape, device, and dtype")
     if lse.shape != (q.shape[0], q.shape[2], q.shape[1]) or lse.dtype != torch.float32 or lse.device != q.device:
         raise ValueError("lse must be float32 [B, Hq, Nq] on q's device")
-    sched = dict(_SCHEDULE)
+    sched = _schedule(q.shape[-1])
     for key, val in (("block_m", block_m), ("block_n", block_n), ("threads", threads), ("num_stages", num_stages)):
         if val is not None:
             sched[key] = val
@@ -217,7 +243,11 @@ def flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, *, softmax_scale=None, ca
         raise ValueError("unsupported tile/pipeline configuration")
     q, k, v = (x.contiguous() for x in (q, k, v))
     tq, tk, tv = (_prepare_tangent(t, p, n) for t, p, n in zip((tq, tk, tv), (q, k, v), ("tq", "tk", "tv")))
-    return _jvp_op(q, k, v, tq, tk, tv, out.contiguous(), lse.contiguous(), scale, bool(causal))
+    empty = q.new_empty(0)
+    tq, tk, tv = (empty if t is None else t for t in (tq, tk, tv))
+    return torch.ops.kernelforge.flash_attention_jvp(q, k, v, tq, tk, tv, out.contiguous(), lse.contiguous(),
+                                                     scale, bool(causal), sched["block_m"], sched["block_n"],
+                                                     sched["threads"], sched["num_stages"])
 
 
 @torch.no_grad()

@@ -18,6 +18,7 @@ from __future__ import annotations
 from functools import lru_cache
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from .. import _lib
 
@@ -136,11 +137,74 @@ def original_tilelang_rms_norm(A: torch.Tensor, blk_m: int = 1) -> torch.Tensor:
     return B
 
 
-class RMSNorm(torch.nn.Module):
-    """``RMSNorm(dim, scale_factor=1.0, eps=1e-6)`` (rmsnorm/original.py:9-52) on the HIP kernel.
+def _promoted(x: torch.Tensor, weight: torch.Tensor) -> torch.dtype:
+    return torch.promote_types(x.dtype, weight.dtype)
 
-    The weight must have the input's dtype (cast the module with ``.to``);
-    mixed-dtype promotion is not implemented and raises ValueError.
+
+class _RMSNormFunction(torch.autograd.Function):
+    """``RMSNorm.forward`` (rmsnorm/original.py:51-52) with torch's dtype
+    promotion, and its gradient, on the HIP kernels (kf_rmsnorm_fwd_mixed,
+    kf_rmsnorm_bwd).  x is normalised over its last dimension."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        lib = _lib.load()
+        x = x.contiguous()
+        weight = weight.contiguous()
+        dim = x.shape[-1]
+        rows = x.numel() // dim
+        out = torch.empty(x.shape, device=x.device, dtype=_promoted(x, weight))
+        rc = lib.kf_rmsnorm_fwd_mixed(_lib.ptr(x), _lib.ptr(weight), _lib.ptr(out), rows, dim, float(eps),
+                                      _lib.kf_dtype(x.dtype), _lib.kf_dtype(weight.dtype),
+                                      _lib.kf_dtype(out.dtype), _lib.stream_of(x))
+        _lib.check(rc, "kf_rmsnorm_fwd_mixed")
+        ctx.save_for_backward(x, weight)
+        ctx.eps = float(eps)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        lib = _lib.load()
+        dim = x.shape[-1]
+        rows = x.numel() // dim
+        dy = dy.contiguous().to(_promoted(x, weight))
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(weight)
+        ws_bytes = int(lib.kf_rmsnorm_bwd_workspace_bytes(rows, dim))
+        ws = torch.empty(max(ws_bytes, 4), device=x.device, dtype=torch.uint8)
+        rc = lib.kf_rmsnorm_bwd(_lib.ptr(x), _lib.ptr(weight), _lib.ptr(dy), _lib.ptr(dx), _lib.ptr(dw),
+                                _lib.ptr(ws), ws_bytes, rows, dim, ctx.eps, _lib.kf_dtype(x.dtype),
+                                _lib.kf_dtype(weight.dtype), _lib.stream_of(x))
+        _lib.check(rc, "kf_rmsnorm_bwd")
+        return dx, dw, None
+
+
+def rms_norm_module_forward(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``RMSNorm.forward`` semantics for any float dtypes of x and weight: the
+    result has dtype ``promote_types(x.dtype, weight.dtype)`` and is
+    differentiable with respect to x and weight."""
+    if x.dim() < 1 or weight.dim() != 1 or weight.shape[0] != x.shape[-1]:
+        raise ValueError("weight must have shape (x.shape[-1],)")
+    for t in (x, weight):
+        if t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise ValueError(f"unsupported dtype {t.dtype}")
+    _lib.require_gpu(x, weight)
+    if weight.device != x.device:
+        raise ValueError("x and weight must be on the same device")
+    return _RMSNormFunction.apply(x, weight, eps)
+
+
+class RMSNorm(torch.nn.Module):
+    """``RMSNorm(dim, scale_factor=1.0, eps=1e-6)`` (rmsnorm/original.py:9-52) on the HIP kernels.
+
+    The weight is an fp32 parameter of ones times ``scale_factor``
+    (original.py:25).  ``forward`` returns ``dt(x * inv) * weight`` with
+    torch's type promotion (original.py:51-52): bf16 input with the default
+    fp32 weight gives an fp32 result; after ``.to(torch.bfloat16)`` the result
+    is bf16.  Gradients with respect to x and the weight run on the HIP
+    backward kernel.
     """
 
     def __init__(self, dim: int, scale_factor=1.0, eps: float = 1e-6):
@@ -149,4 +213,4 @@ class RMSNorm(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.ones(dim) * scale_factor)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return rms_norm_tensor(x, self.weight.detach(), self.eps)
+        return rms_norm_module_forward(x, self.weight, self.eps)

@@ -26,6 +26,19 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.T
     return (normed.float() * weight.float()).to(torch.promote_types(x.dtype, weight.dtype))
 
 
+def rmsnorm_grads(x: torch.Tensor, weight: torch.Tensor, dy: torch.Tensor, eps: float = 1e-6):
+    """``(dx, dweight)`` of ``rmsnorm`` for the output gradient ``dy``, by torch
+    autograd on the CPU through the same operations (rmsnorm/original.py:38,
+    51-52), as the reference module's backward computes them."""
+    x = x.detach().cpu().clone().requires_grad_(True)
+    weight = weight.detach().cpu().clone().requires_grad_(True)
+    xf = x.float() if x.dtype != torch.float64 else x
+    normed = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).type_as(x)
+    out = normed * weight
+    out.backward(dy.detach().cpu().to(out.dtype))
+    return x.grad, weight.grad
+
+
 def rmsnorm_fp64(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """The same formula with every step in fp64 and no intermediate rounding."""
     xd = x.detach().cpu().double()

@@ -11,18 +11,28 @@ def randn(shape, dtype=torch.float32, seed=0, mean=0.0, std=1.0, gen=None):
     return (torch.randn(shape, generator=g, dtype=torch.float32) * std + mean).to(dtype)
 
 
-def bf16_flip_check(actual: torch.Tensor, expected: torch.Tensor, atol=1e-2, max_flip_frac=1e-3):
-    """bf16 RMSNorm parity: |a-e| <= atol + 2^-6 |e| everywhere, and at most
-    `max_flip_frac` of the elements differ at all.
+def bf16_flip_check(actual: torch.Tensor, expected: torch.Tensor, max_flip_frac: float = 1e-6,
+                    atol: float = 1e-2):
+    """bf16 RMSNorm parity against the oracle's bf16 result.
 
-    A differing element comes from the fp32 summation order of the sum of
-    squares: `inv` one fp32 ulp away flips the first rounding point dt(x*inv)
-    by one bf16 ulp (2^-7 relative at most), which the weight multiply and the
-    second rounding can carry to two ulps of y, i.e. 2^-6 |y|.
+    Elements equal bit for bit except at most ``max_flip_frac`` of them (at
+    least one element is never granted: a 10-element tensor with cap 2e-5
+    must match exactly).  A differing element comes from the fp32 summation
+    order of the sum of squares: ``inv`` one fp32 ulp away flips the first
+    rounding point dt(x*inv) by one bf16 ulp, which the weight multiply and
+    the second rounding can carry to two ulps of y, so every differing
+    element must lie within 2^-6 |e| (two bf16 ulps) of the oracle.  Elements
+    that agree meet the north-star ``atol`` trivially; it is asserted over
+    all elements with |e| < 0.5, where two ulps are below it.
     Returns (max_abs_err, n_diff)."""
     a = actual.detach().float().cpu()
     e = expected.detach().float().cpu()
-    torch.testing.assert_close(a, e, atol=atol, rtol=2.0 ** -6)
-    n_diff = int((a != e).sum())
+    assert a.shape == e.shape
+    diff = (a - e).abs()
+    flipped = diff > 0
+    n_diff = int(flipped.sum())
     assert n_diff <= max_flip_frac * a.numel(), f"{n_diff} of {a.numel()} elements differ"
-    return float((a - e).abs().max()) if a.numel() else 0.0, n_diff
+    assert bool((diff[flipped] <= 2.0 ** -6 * e.abs()[flipped] + 1e-30).all()), "a flip exceeds two ulps"
+    small = e.abs() < 0.5
+    assert float(diff[small].max()) <= atol if bool(small.any()) else True
+    return float(diff.max()) if a.numel() else 0.0, n_diff

@@ -5,6 +5,8 @@ double precision with a *different algorithm* from the oracle's, so that they
 pin the oracle rather than restate it:
 
 - RMSNorm: y = x / sqrt(fsum(x^2)/n + eps) * w           (rmsnorm/original.py:38,51-52)
+- RMSNorm bf16: the same with fp32 operations emulated by explicit rounding
+           and the two bf16 rounding points of original.py:51-52
 - SANA:    the O(N^2) quadratic form
            out[n][r] = sum_m (q_n . k_m) v_m[r] / (sum_m q_n . k_m + eps),
            q, k after ReLU -- algebraically equal to the linear form of
@@ -25,6 +27,7 @@ from __future__ import annotations
 import json
 import math
 import random
+import struct
 from pathlib import Path
 
 HERE = Path(__file__).resolve().parent
@@ -55,6 +58,44 @@ def rmsnorm_cases():
             inv = 1.0 / math.sqrt(math.fsum(v * v for v in row) / dim + eps)
             y.append([row[c] * inv * w[c] for c in range(dim)])
         cases.append(dict(rows=rows, dim=dim, eps=eps, x=x, w=w, y=y))
+    return cases
+
+
+def f32(x: float) -> float:
+    """Round a double to the nearest fp32 value (ties to even)."""
+    return struct.unpack("<f", struct.pack("<f", x))[0]
+
+
+def rmsnorm_bf16_cases():
+    """bf16 RMSNorm with both rounding points of rmsnorm/original.py:51-52.
+
+    Each row is drawn so that its sum of squares is exact in fp32 and its
+    length is a power of two; the mean, ``+ eps``, ``sqrt`` and ``1/`` are
+    then single fp32 operations, evaluated here in double and rounded to fp32
+    (correct for these operations, since 53 >= 2*24 + 2).  Then
+    ``n = bf16(f32(x * inv))`` (first rounding) and
+    ``y = bf16(f32(n * w))`` (second rounding).  ``y_single`` is the same
+    computation with one rounding at the end, ``bf16(f32(f32(x * inv) * w))``;
+    each case holds elements where the two differ, so a kernel or oracle that
+    drops the first rounding fails the fixture.
+    """
+    cases = []
+    for seed, (rows, dim, eps) in enumerate([(4, 8, 1e-6), (3, 16, 1e-6), (2, 64, 1e-5), (2, 32, 1e-6)]):
+        rng = random.Random(400 + seed)
+        x, y, y_single = [], [], []
+        w = draw(rng, dim, 1.0, 0.1)
+        while len(x) < rows:
+            row = draw(rng, dim, 0.0, 1.0)
+            ss = math.fsum(v * v for v in row)
+            if f32(ss) != ss:
+                continue  # keep rows whose fp32 sum of squares is exact in any order
+            inv = f32(1.0 / f32(math.sqrt(f32(f32(ss / dim) + f32(eps)))))
+            n = [bf16_round(f32(v * inv)) for v in row]
+            x.append(row)
+            y.append([bf16_round(f32(n[c] * w[c])) for c in range(dim)])
+            y_single.append([bf16_round(f32(f32(row[c] * inv) * w[c])) for c in range(dim)])
+        assert any(a != b for ra, rb in zip(y, y_single) for a, b in zip(ra, rb)), "no double-rounding case"
+        cases.append(dict(rows=rows, dim=dim, eps=eps, x=x, w=w, y=y, y_single=y_single))
     return cases
 
 
@@ -128,7 +169,8 @@ def fa_cases():
 
 
 def main():
-    for name, fn in (("rmsnorm", rmsnorm_cases), ("sana", sana_cases), ("fa", fa_cases)):
+    for name, fn in (("rmsnorm", rmsnorm_cases), ("rmsnorm_bf16", rmsnorm_bf16_cases), ("sana", sana_cases),
+                     ("fa", fa_cases)):
         path = HERE / f"{name}_golden.json"
         path.write_text(json.dumps(fn(), allow_nan=True))
         print(f"wrote {path} ({path.stat().st_size} bytes)")

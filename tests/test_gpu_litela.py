@@ -26,6 +26,27 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(autouse=True)
+def _forward_only():
+    """The modules are forward-only (no backward kernels): every test runs under
+    no_grad, as the reference's tests run under inference_mode."""
+    with torch.no_grad():
+        yield
+
+
+def test_modules_refuse_to_record_autograd():
+    m = LiteLA(64, 64).to(DEV)
+    x = torch.randn(1, 16, 64, device=DEV)
+    with torch.enable_grad():
+        with pytest.raises(RuntimeError, match="no backward"):
+            m(x)
+        m.requires_grad_(False)
+        with pytest.raises(RuntimeError, match="no backward"):
+            m(x.requires_grad_(True))
+        y = m(x.detach())  # frozen module, plain input: allowed
+    assert y.shape == (1, 16, 64) and not y.requires_grad
+
+
 def _module_ref(m, x, qk_norm, rotary_emb=None):
     return osana.lite_la_forward(
         x.cpu(), m.qkv.weight, m.qkv.bias, m.proj.weight, m.proj.bias, m.heads, m.eps,

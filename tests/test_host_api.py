@@ -115,3 +115,47 @@ def test_litela_variants_on_the_host():
         pw = torch.empty(256, 256, dtype=torch.bfloat16)
         y = modules._joint_litela_op_fake(x, w, None, pw, None, None, None, 8, 32, 1e-15, 1e-5)
         assert y.shape == (2, 64, 256) and y.dtype == torch.bfloat16
+
+
+def test_reference_jvp_operator_schema():
+    """kernelforge::flash_attention_jvp is registered with the reference's schema
+    (flash_attention_jvp/custom.py:137-157) and has a fake implementation."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    op = torch.ops.kernelforge.flash_attention_jvp.default
+    schema = op._schema
+    names = [a.name for a in schema.arguments]
+    assert names == ["q", "k", "v", "tq", "tk", "tv", "out", "lse", "scale", "causal", "block_m", "block_n",
+                     "threads", "num_stages"]
+    types = [str(a.type) for a in schema.arguments]
+    assert types == ["Tensor"] * 8 + ["float", "bool", "int", "int", "int", "int"]
+    assert [str(r.type) for r in schema.returns] == ["Tensor"]
+    with FakeTensorMode():
+        q = torch.empty(1, 9, 2, 64, dtype=torch.bfloat16)
+        k = torch.empty(1, 13, 2, 64, dtype=torch.bfloat16)
+        lse = torch.empty(1, 2, 9, dtype=torch.float32)
+        t = op(q, k, k, q, k, k, q, lse, 0.125, False, 64, 64, 128, 2)
+        assert t.shape == q.shape and t.dtype == q.dtype
+
+
+def test_jvp_schedule_reports_the_kernel_tile():
+    assert fa._schedule(64) == dict(block_m=128, block_n=64, threads=512, num_stages=2)
+    assert fa._schedule(128) == dict(block_m=128, block_n=64, threads=512, num_stages=2)
+    assert fa._schedule(136) == dict(block_m=64, block_n=32, threads=256, num_stages=2)
+    assert fa._schedule(256) == dict(block_m=64, block_n=32, threads=256, num_stages=2)
+    for key, values in fa._ALLOWED.items():
+        for d in (64, 256):
+            assert fa._schedule(d)[key] in values
+
+
+def test_rmsnorm_module_host_side():
+    """The module keeps the reference's fp32 parameter (rmsnorm/original.py:25) and
+    rejects CPU tensors instead of computing them."""
+    from kernelforge_amd.rmsnorm import RMSNorm
+
+    m = RMSNorm(64, scale_factor=2.0)
+    assert m.weight.dtype == torch.float32 and bool((m.weight == 2.0).all())
+    with pytest.raises(ValueError, match="device"):
+        m(torch.zeros(3, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="shape"):
+        m(torch.zeros(3, 32))

@@ -55,6 +55,65 @@ def test_rmsnorm_unit_rms_and_scale_equivariance():
     torch.testing.assert_close(a.double(), y, rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("case", load("rmsnorm_bf16"), ids=lambda c: f"{c['rows']}x{c['dim']}")
+def test_rmsnorm_bf16_two_rounding_points(case):
+    """The oracle in bf16 reproduces the fixture's two rounding points bit for bit."""
+    x = torch.tensor(case["x"], dtype=torch.float64).bfloat16()
+    w = torch.tensor(case["w"], dtype=torch.float64).bfloat16()
+    y = torch.tensor(case["y"], dtype=torch.float64).bfloat16()
+    assert torch.equal(x.double(), torch.tensor(case["x"], dtype=torch.float64))  # exact in bf16
+    out = orms.rmsnorm(x, w, case["eps"])
+    assert out.dtype == torch.bfloat16
+    assert torch.equal(out, y)
+
+
+def test_mutation_rmsnorm_single_rounding():
+    """A restatement that rounds once (dropping the cast before the weight
+    multiply, original.py:51) fails the double-rounding fixture."""
+    def single_rounding(x, w, eps):
+        xf = x.float()
+        inv = 1.0 / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return (xf * inv * w.float()).to(x.dtype)
+
+    failures = 0
+    for case in load("rmsnorm_bf16"):
+        x = torch.tensor(case["x"], dtype=torch.float64).bfloat16()
+        w = torch.tensor(case["w"], dtype=torch.float64).bfloat16()
+        y = torch.tensor(case["y"], dtype=torch.float64).bfloat16()
+        y_single = torch.tensor(case["y_single"], dtype=torch.float64).bfloat16()
+        bad = single_rounding(x, w, case["eps"])
+        assert torch.equal(bad, y_single)
+        failures += int(not torch.equal(bad, y))
+    assert failures == len(load("rmsnorm_bf16"))
+
+
+def test_rmsnorm_promotion_and_gradients():
+    """bf16 x with an fp32 weight returns fp32 (torch promotion, original.py:52);
+    the autograd gradients of the oracle agree with central differences of the
+    fp64 formula."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(3, 40, generator=g).bfloat16()
+    w = 1 + 0.1 * torch.randn(40, generator=g)
+    y = orms.rmsnorm(x, w, 1e-6)
+    assert y.dtype == torch.float32
+    assert torch.equal(y, (orms.rmsnorm(x, torch.ones(40), 1e-6)) * w)
+    x64 = torch.randn(3, 40, generator=g, dtype=torch.float64)
+    w64 = 1 + 0.1 * torch.randn(40, generator=g, dtype=torch.float64)
+    dy = torch.randn(3, 40, generator=g, dtype=torch.float64)
+    dx, dw = orms.rmsnorm_grads(x64, w64, dy, 1e-6)
+    e = 1e-6
+    for i, j in ((0, 0), (1, 17), (2, 39)):
+        d = torch.zeros_like(x64)
+        d[i, j] = e
+        fd = ((orms.rmsnorm_fp64(x64 + d, w64, 1e-6) - orms.rmsnorm_fp64(x64 - d, w64, 1e-6)) * dy).sum() / (2 * e)
+        assert abs(float(fd) - float(dx[i, j])) < 1e-7
+    for j in (0, 21):
+        d = torch.zeros_like(w64)
+        d[j] = e
+        fd = ((orms.rmsnorm_fp64(x64, w64 + d, 1e-6) - orms.rmsnorm_fp64(x64, w64 - d, 1e-6)) * dy).sum() / (2 * e)
+        assert abs(float(fd) - float(dw[j])) < 1e-7
+
+
 def test_mutation_rmsnorm_mean_vs_sum():
     case = load("rmsnorm")[0]
     x, w, y = t64(case["x"]), t64(case["w"]), t64(case["y"])
