@@ -6,7 +6,8 @@ pin the oracle rather than restate it:
 
 - RMSNorm: y = x / sqrt(fsum(x^2)/n + eps) * w           (rmsnorm/original.py:38,51-52)
 - RMSNorm bf16: the same with fp32 operations emulated by explicit rounding
-           and the two bf16 rounding points of original.py:51-52
+           and the two bf16 rounding points of original.py:51-52; and rows
+           whose output flips if 1/sqrt is one fp32 ulp off (rmsnorm_inv)
 - SANA:    the O(N^2) quadratic form
            out[n][r] = sum_m (q_n . k_m) v_m[r] / (sum_m q_n . k_m + eps),
            q, k after ReLU -- algebraically equal to the linear form of
@@ -99,6 +100,58 @@ def rmsnorm_bf16_cases():
     return cases
 
 
+def f32_step(x: float, ulps: int) -> float:
+    """The fp32 value `ulps` representable steps away from the fp32 value x (x > 0)."""
+    bits = struct.unpack("<I", struct.pack("<f", x))[0]
+    return struct.unpack("<f", struct.pack("<I", bits + ulps))[0]
+
+
+def rmsnorm_inv_cases():
+    """Rows whose bf16 output changes if 1/sqrt(mean + eps) is one fp32 ulp off.
+
+    The values are multiples of 1/16 with |x| <= 2.5, so the fp32 sum of squares
+    is exact in any order and mean = ss/64 is exact; eps (an fp32 value) is
+    tuned so that some x_j * inv lands next to a bf16 rounding midpoint, where
+    a one-ulp change of inv in the recorded direction flips bf16(x_j * inv).
+    inv = f32(1 / f32(sqrt(f32(mean + eps)))), correctly rounded as above.
+    ``y_off`` is the output with inv moved one ulp in ``direction``: it differs
+    from ``y``, so these rows pin a correctly rounded inverse square root.
+    """
+    rng = random.Random(500)
+    dim = 64
+    cases = []
+    for direction in (1, -1) * 4:
+        found = None
+        while found is None:
+            row = [rng.randint(-40, 40) / 16 for _ in range(dim)]
+            mean = math.fsum(v * v for v in row) / dim
+            w = [bf16_round(1.0 + rng.randint(-8, 8) / 64) for _ in range(dim)]
+            for j in rng.sample(range(dim), dim):
+                if row[j] == 0.0:
+                    continue
+                mant, ex = math.frexp(row[j] / math.sqrt(mean + 1e-2))
+                mid = math.copysign((math.floor(abs(mant) * 256) + 0.5) / 256, mant) * 2.0 ** ex
+                eps0 = (row[j] / mid) ** 2 - mean
+                if eps0 <= 1e-3:
+                    continue
+                for d in range(-100, 101):
+                    eps = f32_step(f32(eps0), d)
+                    inv = f32(1.0 / f32(math.sqrt(f32(mean + eps))))
+                    n = [bf16_round(f32(v * inv)) for v in row]
+                    off = f32_step(inv, direction)
+                    n_off = [bf16_round(f32(v * off)) for v in row]
+                    if n != n_off:
+                        y = [bf16_round(f32(n[c] * w[c])) for c in range(dim)]
+                        y_off = [bf16_round(f32(n_off[c] * w[c])) for c in range(dim)]
+                        found = dict(rows=1, dim=dim, eps=eps, direction=direction, x=[row], w=w, y=[y],
+                                     y_off=[y_off])
+                        break
+                if found is not None:
+                    break
+        cases.append(found)
+    return cases
+
+
 def sana_cases():
     cases = []
     for seed, (B, N, H, D) in enumerate([(1, 5, 2, 4), (2, 7, 1, 3), (1, 1, 3, 2), (1, 9, 2, 8)]):
@@ -169,8 +222,8 @@ def fa_cases():
 
 
 def main():
-    for name, fn in (("rmsnorm", rmsnorm_cases), ("rmsnorm_bf16", rmsnorm_bf16_cases), ("sana", sana_cases),
-                     ("fa", fa_cases)):
+    for name, fn in (("rmsnorm", rmsnorm_cases), ("rmsnorm_bf16", rmsnorm_bf16_cases),
+                     ("rmsnorm_inv", rmsnorm_inv_cases), ("sana", sana_cases), ("fa", fa_cases)):
         path = HERE / f"{name}_golden.json"
         path.write_text(json.dumps(fn(), allow_nan=True))
         print(f"wrote {path} ({path.stat().st_size} bytes)")

@@ -45,6 +45,8 @@ def test_bf16_llm_sweep(hidden):
     x, w = _inputs(16384, hidden, torch.bfloat16, seed=hidden)
     y = custom_rms_norm(1, 16384, hidden, 1e-6, "bfloat16")(x[None].to(DEV), w.to(DEV))[0]
     ref = orc.rmsnorm(x, w, 1e-6)
+    # Summation-order flips only (see bf16_flip_check); the precision of inv
+    # itself is pinned bit for bit by test_inverse_sqrt_sensitive_rows.
     err, n_diff = bf16_flip_check(y, ref)
     print(f"hidden={hidden} max_abs_err={err:.3g} differing={n_diff}")
     # Against the unrounded fp64 formula the error is bounded by the two roundings.
@@ -63,7 +65,7 @@ def test_shapes_and_dtypes(rows, dim, dtype):
     if dtype == torch.float32:
         torch.testing.assert_close(y.cpu(), ref, rtol=1e-5, atol=0)
     elif dtype == torch.bfloat16:
-        bf16_flip_check(y, ref, max_flip_frac=2e-5)
+        bf16_flip_check(y, ref)
     else:
         torch.testing.assert_close(y.cpu().float(), ref.float(), atol=1e-3, rtol=2.0 ** -10)
 
@@ -76,7 +78,7 @@ def test_unaligned_views_and_empty():
     y = RMSNorm(256).to(DEV, torch.bfloat16)
     y.weight.data.copy_(w[1:].to(DEV))
     out = y(sub)
-    bf16_flip_check(out, orc.rmsnorm(x[:, 1:], w[1:]), max_flip_frac=2e-5)
+    bf16_flip_check(out, orc.rmsnorm(x[:, 1:], w[1:]))
     empty = custom_rms_norm(1, 0, 64, 1e-6, "bfloat16")(torch.empty(1, 0, 64, device=DEV,
                                                                     dtype=torch.bfloat16),
                                                         torch.ones(64, device=DEV, dtype=torch.bfloat16))
@@ -113,6 +115,20 @@ def test_shape_validation():
           torch.ones(32, device=DEV, dtype=torch.bfloat16))
 
 
+def test_inverse_sqrt_sensitive_rows():
+    """Rows whose bf16 output flips if inv = 1/sqrt(mean + eps) is one fp32 ulp
+    off (tests/golden/rmsnorm_inv_golden.json; exact sums of squares, so the
+    summation order cannot matter): bit for bit.  An approximate reciprocal
+    square root (v_rsq_f32) would miss some of them."""
+    cases = json.loads((Path(__file__).resolve().parent / "golden" / "rmsnorm_inv_golden.json").read_text())
+    for case in cases:
+        x = torch.tensor(case["x"], dtype=torch.float64).bfloat16()
+        w = torch.tensor(case["w"], dtype=torch.float64).bfloat16()
+        y = torch.tensor(case["y"], dtype=torch.float64).bfloat16()
+        out = custom_rms_norm(1, 1, case["dim"], case["eps"], "bfloat16")(x[None].to(DEV), w.to(DEV))[0]
+        assert torch.equal(out.cpu(), y), case["eps"]
+
+
 def test_double_rounding_fixture():
     """The pure-Python fixture with both bf16 rounding points (tests/golden,
     rmsnorm_bf16_golden.json): bit for bit, and not the single-rounding values."""
@@ -140,11 +156,13 @@ def test_default_module_promotes_to_fp32(xdtype):
     assert y.dtype == torch.float32
     ref = orc.rmsnorm(x, m.weight.detach().cpu(), 1e-6)
     assert ref.dtype == torch.float32
-    # fp32 result of a 16-bit first rounding: equal except for flips of that
-    # rounding (one 16-bit ulp of n, times |w|).
+    # fp32 result of a 16-bit first rounding: equal except for summation-order
+    # flips of that rounding (one 16-bit ulp of n, times |w|), whose rate is
+    # ~2^-16 per element for bf16 and ~2^-13 for fp16 (finer grid).
     diff = (y.cpu() - ref).abs()
     ulp = 2.0 ** -7 if xdtype == torch.bfloat16 else 2.0 ** -10
-    assert int((diff > 0).sum()) <= 1e-6 * diff.numel() + 1
+    lam = (1e-5 if xdtype == torch.bfloat16 else 2e-4) * diff.numel()
+    assert int((diff > 0).sum()) <= lam + 4 * lam ** 0.5 + 3
     assert bool((diff <= ulp * ref.abs() * 1.01 + 1e-30).all())
     torch.testing.assert_close(y.cpu(), ref, atol=1e-2, rtol=0)
 

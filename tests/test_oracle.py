@@ -67,6 +67,23 @@ def test_rmsnorm_bf16_two_rounding_points(case):
     assert torch.equal(out, y)
 
 
+@pytest.mark.parametrize("case", load("rmsnorm_inv"), ids=lambda c: f"eps{c['eps']:.4g}dir{c['direction']}")
+def test_rmsnorm_inverse_sqrt_is_correctly_rounded(case):
+    """Rows where a one-ulp error of 1/sqrt(mean + eps) flips a bf16 output: the
+    oracle gives the fixture's bits, and the same computation with inv moved
+    one ulp in the recorded direction gives the fixture's ``y_off`` instead."""
+    x = torch.tensor(case["x"], dtype=torch.float64).bfloat16()
+    w = torch.tensor(case["w"], dtype=torch.float64).bfloat16()
+    y = torch.tensor(case["y"], dtype=torch.float64).bfloat16()
+    y_off = torch.tensor(case["y_off"], dtype=torch.float64).bfloat16()
+    assert torch.equal(orms.rmsnorm(x, w, case["eps"]), y)
+    xf = x.float()
+    inv = 1.0 / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + case["eps"])
+    off = torch.nextafter(inv, torch.full_like(inv, math.inf if case["direction"] > 0 else -math.inf))
+    bad = ((xf * off).bfloat16().float() * w.float()).bfloat16()
+    assert torch.equal(bad, y_off) and not torch.equal(bad, y)
+
+
 def test_mutation_rmsnorm_single_rounding():
     """A restatement that rounds once (dropping the cast before the weight
     multiply, original.py:51) fails the double-rounding fixture."""
