@@ -171,6 +171,32 @@ int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
                    int in_dtype, int out_dtype, kf_stream_t stream);
 
 /*
+ * Largest scratch, in bytes, that kf_linattn_fwd_noalloc can use: the size
+ * of its static device array (16 MiB), which must hold
+ * kf_linattn_workspace_bytes(batch, heads, dim, splits).
+ */
+int64_t kf_linattn_noalloc_max_bytes(void);
+
+/*
+ * kf_linattn_fwd without a workspace argument and without any allocation:
+ * the split partials and reduced states live in a static device array of
+ * kf_linattn_noalloc_max_bytes() bytes that each GPU holds until the process
+ * ends.  No counterpart in the reference; it exists for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, kernels and results as kf_linattn_fwd
+ * with the same splits (splits <= 0 selects kf_linattn_default_splits).
+ * Returns KF_E_WORKSPACE, before any device work, when the request needs more
+ * scratch than the array holds (pass fewer splits or use kf_linattn_fwd).
+ * Every call on one GPU shares that GPU's array, so calls that overlap on
+ * one GPU (concurrent streams or threads) race and must be serialised by the
+ * caller.  The array keeps the last call's contents; nothing in it needs to
+ * start at zero (every call writes all it later reads).
+ */
+int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
+                           int64_t heads, int64_t dim, int64_t splits, float eps,
+                           int in_dtype, int out_dtype, kf_stream_t stream);
+
+/*
  * Rotary position embedding, in place on the q and k parts of a packed
  * qkv[batch, seq_len, 3, heads*dim] buffer (v untouched): within each head,
  * channels (2i, 2i+1) rotate as a complex pair by the angle whose cosine and

@@ -48,6 +48,9 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int,
          _c_void_p],
     ),
+    "kf_linattn_noalloc_max_bytes": (_i64, []),
+    "kf_linattn_fwd_noalloc": (
+        _int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p]),
     "kf_rope_packed": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "kf_fa_fwd": (
         _int,

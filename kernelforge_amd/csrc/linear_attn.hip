@@ -27,6 +27,15 @@
 // three stages and the same fixed-order split reduction.
 #include "kf_common.h"
 
+#include <mutex>
+
+// Device scratch of kf_linattn_fwd_noalloc: the split partials and reduced
+// states live here instead of in a caller workspace.  Each GPU the library
+// runs on holds its own copy until the process ends; host code reaches it
+// only through the per-device address from hipGetSymbolAddress.
+constexpr int64_t kLinattnScratchBytes = 16LL << 20;
+static __device__ __align__(256) unsigned char scratch[kLinattnScratchBytes];
+
 namespace kf {
 namespace {
 
@@ -595,11 +604,14 @@ extern "C" int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int6
     return (int64_t)sizeof(float) * batch * heads * state * (splits + 1);
 }
 
-extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64_t workspace_bytes,
-                              int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
-                              int64_t splits, float eps, int in_dtype, int out_dtype,
-                              kf_stream_t stream) {
-    using namespace kf;
+namespace kf {
+namespace {
+
+// Validates the request, resolves the split count and runs the three
+// stages with `workspace` holding the partials and the reduced states.
+int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_bytes, int64_t batch,
+                int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
+                int out_dtype, hipStream_t s) {
     KF_REQUIRE(batch >= 0 && seq_len >= 0 && heads >= 0, KF_E_INVALID,
                "linattn: negative shape B=%lld N=%lld H=%lld", (long long)batch,
                (long long)seq_len, (long long)heads);
@@ -628,7 +640,6 @@ extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64
     const int64_t state_size = (dim + 1) * dim;
     float* partial = static_cast<float*>(workspace);
     float* state = partial + batch * heads * state_size * splits;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const int B = (int)batch, N = (int)seq_len, H = (int)heads, D = (int)dim;
     const int S = (int)eff_splits, L = (int)split_len;
     switch (in_dtype) {
@@ -636,4 +647,59 @@ extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64
         case KF_F16: return run_in<f16>(out_dtype, mfma, D, qkv, out, partial, state, B, N, H, S, L, eps, s);
         default: return run_in<float>(out_dtype, false, D, qkv, out, partial, state, B, N, H, S, L, eps, s);
     }
+}
+
+// Per-device address of `scratch`, resolved once per device with that
+// device current (each GPU holds its own copy at its own address).
+int scratch_for_current_device(void** ptr) {
+    static std::mutex lock;
+    static void* addr[64] = {};
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return hip_failure(err, "linattn: hipGetDevice");
+    KF_REQUIRE(dev >= 0 && dev < 64, KF_E_UNSUPPORTED, "linattn: device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> guard(lock);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return hip_failure(err, "linattn: hipGetSymbolAddress(scratch)");
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return KF_OK;
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64_t workspace_bytes,
+                              int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
+                              int64_t splits, float eps, int in_dtype, int out_dtype,
+                              kf_stream_t stream) {
+    return kf::linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps,
+                           in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t kf_linattn_noalloc_max_bytes(void) { return kLinattnScratchBytes; }
+
+extern "C" int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
+                                      int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
+                                      int out_dtype, kf_stream_t stream) {
+    using namespace kf;
+    // Size check first, so an oversized request fails before any device call.
+    int64_t eff = splits <= 0 ? kf_linattn_default_splits(batch, heads, dim, seq_len) : splits;
+    if (eff > seq_len && seq_len > 0) eff = seq_len;
+    const int64_t need = kf_linattn_workspace_bytes(batch, heads, dim, eff);
+    KF_REQUIRE(need <= kLinattnScratchBytes, KF_E_WORKSPACE,
+               "linattn noalloc: %lld bytes of scratch needed for B=%lld H=%lld D=%lld splits=%lld, "
+               "the static scratch holds %lld; use fewer splits or kf_linattn_fwd with a workspace",
+               (long long)need, (long long)batch, (long long)heads, (long long)dim, (long long)eff,
+               (long long)kLinattnScratchBytes);
+    if (batch <= 0 || seq_len <= 0 || heads <= 0)
+        return linattn_run(qkv, out, nullptr, 0, batch, seq_len, heads, dim, eff, eps, in_dtype, out_dtype,
+                           static_cast<hipStream_t>(stream));
+    void* ws = nullptr;
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+    return linattn_run(qkv, out, ws, kLinattnScratchBytes, batch, seq_len, heads, dim, eff, eps, in_dtype,
+                       out_dtype, static_cast<hipStream_t>(stream));
 }
