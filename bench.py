@@ -136,6 +136,7 @@ def bench_sana(B: int, H: int, N: int, steps: int, warmup: int, D: int = 32) -> 
     ws_bytes = int(lib.kf_linattn_workspace_bytes(B, H, D, splits))
     ws = torch.empty(ws_bytes, device="cuda", dtype=torch.uint8)
     stream = _lib.stream_of(ws)
+    _lib.check(lib.kf_linattn_workspace_init(_lib.ptr(ws), ws_bytes, stream), "kf_linattn_workspace_init")
     args = [(_lib.ptr(qkvs[i]), _lib.ptr(outs[i])) for i in range(n_sets)]
     wsp = _lib.ptr(ws)
     fnc = lib.kf_linattn_fwd
@@ -149,7 +150,7 @@ def bench_sana(B: int, H: int, N: int, steps: int, warmup: int, D: int = 32) -> 
     us, n_warm = _time_launches(launch, n_sets, steps, warmup)
     gbs = bytes_per_launch / (us * 1e-6) / 1e9
     tflops = flops / (us * 1e-6) / 1e12
-    return dict(kernel="linattn (state+reduce+out)", workload=f"sana_bf16_B{B}_H{H}_D{D}_N{N}", us=us,
+    return dict(kernel="linattn_fused_kernel", workload=f"sana_bf16_B{B}_H{H}_D{D}_N{N}", us=us,
                 warmup_launches=n_warm, steps=steps,
                 bytes=bytes_per_launch, flops=flops, gbs=gbs, tflops=tflops,
                 roofline_frac=gbs / HBM_PEAK_GBS, mfma_frac=tflops / BF16_PEAK_TFLOPS, splits=splits,

@@ -143,9 +143,23 @@ int kf_rmsnorm_noweight_f32(const float* a, float* b, int64_t rows, int64_t n,
 int64_t kf_linattn_default_splits(int64_t batch, int64_t heads, int64_t dim,
                                   int64_t seq_len);
 
-/* Workspace bytes kf_linattn_fwd needs for `splits` sequence splits. */
+/*
+ * Workspace bytes kf_linattn_fwd needs for `splits` sequence splits: a fixed
+ * region of control words (arrival counters of the fused kernel), then the
+ * fp32 split partials [B, H, splits, D+1, D] and the reduced states.
+ */
 int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int64_t dim,
                                    int64_t splits);
+
+/*
+ * Prepare a new SANA workspace: zeroes its control words on `stream`.  A
+ * workspace's control words must be zero before its first kf_linattn_fwd
+ * call (memory from a zeroing allocator needs no init); every call leaves
+ * them zero again, so a workspace is initialised once and then reused for
+ * any shape it is large enough for.  Calls sharing a workspace must be
+ * ordered (one stream, or synchronised streams).
+ */
+int kf_linattn_workspace_init(void* workspace, int64_t workspace_bytes, kf_stream_t stream);
 
 /*
  * out[b, n, h*D + r] = sum_c S[r][c] relu(q)[n,c] / (sum_c z[c] relu(q)[n,c] + eps)
@@ -162,8 +176,13 @@ int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int64_t dim,
  *
  * qkv: [batch, seq_len, 3, heads*dim] of in_dtype (KF_BF16 or KF_F16, or KF_F32);
  * out: [batch, seq_len, heads*dim] of out_dtype (KF_F32, KF_F16 or KF_BF16).
- * dim must be 32 for the MFMA kernels in this build.
- * splits <= 0 selects kf_linattn_default_splits.
+ * dim must be 32 for the MFMA kernel in this build (one launch: the split
+ * workgroups of a (batch, head pair) meet at a counter in the workspace's
+ * control words); other head dims and fp32 input take a three-launch VALU
+ * path.  splits <= 0 selects kf_linattn_default_splits.
+ * workspace: at least kf_linattn_workspace_bytes bytes, 256-byte aligned,
+ * control words zero on entry (kf_linattn_workspace_init); they are zero
+ * again on return.
  */
 int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
                    int64_t workspace_bytes, int64_t batch, int64_t seq_len,
@@ -189,8 +208,9 @@ int64_t kf_linattn_noalloc_max_bytes(void);
  * scratch than the array holds (pass fewer splits or use kf_linattn_fwd).
  * Every call on one GPU shares that GPU's array, so calls that overlap on
  * one GPU (concurrent streams or threads) race and must be serialised by the
- * caller.  The array keeps the last call's contents; nothing in it needs to
- * start at zero (every call writes all it later reads).
+ * caller.  The array keeps the last call's contents; its control words start
+ * at zero (the first call on a device zeroes them with a fill kernel on the
+ * caller's stream) and every call leaves them zero.
  */
 int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
                            int64_t heads, int64_t dim, int64_t splits, float eps,

@@ -7,13 +7,18 @@ the arithmetic of ``LiteLA.attn_matmul`` (SANA_LinearAttention/original.py:
 99-117) in fp32: ``out = S relu(q) / (z . relu(q) + eps)`` with
 ``S = v^T relu(k)`` and ``z = sum relu(k)`` per (batch, head).
 
-The HIP pipeline (kernelforge_amd/csrc/linear_attn.hip) builds per-split
-states on MFMA, reduces them across splits in a fixed order (deterministic),
-then contracts the state with relu(q) on MFMA.  The split partials live in a
-workspace taken from torch's caching allocator on every call.
+The HIP kernel (kernelforge_amd/csrc/linear_attn.hip) builds per-split
+states on MFMA, lets the split workgroups of each (batch, head pair) meet at
+a counter, sums their partials in a fixed order (deterministic) and
+contracts the state with relu(q) on MFMA, all in one launch.  The counters
+and partials live in a workspace kept per (device, stream): allocated zeroed
+once, grown when a call needs more, and left with zero counters by every
+call.
 """
 
 from __future__ import annotations
+
+import threading
 
 import torch
 
@@ -28,6 +33,23 @@ OUTPUT_DTYPES = ("float", "float16", "bfloat16")
 def default_splits(batch: int, heads: int, dim: int, seq_len: int) -> int:
     """Sequence split count of the state producer for this shape."""
     return int(_lib.load().kf_linattn_default_splits(batch, heads, dim, seq_len))
+
+
+_ws_lock = threading.Lock()
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The zero-initialised workspace of the current stream on `device`, at
+    least `nbytes` long (its control words are zero between calls)."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    with _ws_lock:
+        ws = _workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
+            _workspaces[key] = ws
+    return ws
 
 
 def linear_attention(qkv: torch.Tensor, heads: int, dim: int, eps: float = 1e-15,
@@ -47,8 +69,8 @@ def linear_attention(qkv: torch.Tensor, heads: int, dim: int, eps: float = 1e-15
     if splits is None:
         splits = int(lib.kf_linattn_default_splits(B, heads, dim, N))
     ws_bytes = int(lib.kf_linattn_workspace_bytes(B, heads, dim, splits))
-    ws = torch.empty(ws_bytes, device=qkv.device, dtype=torch.uint8)
-    rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), _lib.ptr(ws), ws_bytes, B, N, heads, dim,
+    ws = _workspace(qkv.device, ws_bytes)
+    rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), _lib.ptr(ws), ws.numel(), B, N, heads, dim,
                             splits, float(eps), _lib.kf_dtype(qkv.dtype), _lib.kf_dtype(output_dtype),
                             _lib.stream_of(qkv))
     _lib.check(rc, "kf_linattn_fwd")
@@ -60,9 +82,9 @@ def qkv_attn_matmul(batch: int, heads: int, dim: int, seq_len: int, eps: float =
     """Return ``run(qkv) -> out`` for one shape (SANA_LinearAttention/custom.py:340-388).
 
     ``reduce_splits`` selected the reference's 3-kernel or 2-kernel schedule;
-    both compute the same values.  This build always reduces the split
-    partials in a separate fixed-order pass, so the flag is accepted for API
-    compatibility only.
+    both compute the same values.  This build always combines the split
+    partials inside its one fused launch, in a fixed order, so the flag is
+    accepted for API compatibility only.
     """
     if dim <= 0 or dim > THREADS or THREADS % dim != 0:
         raise ValueError(f"dim must divide {THREADS} and be at most {THREADS}")

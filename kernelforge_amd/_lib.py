@@ -43,6 +43,7 @@ SIGNATURES = {
                _int, _int, _c_void_p]),
     "kf_linattn_default_splits": (_i64, [_i64, _i64, _i64, _i64]),
     "kf_linattn_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "kf_linattn_workspace_init": (_int, [_c_void_p, _i64, _c_void_p]),
     "kf_linattn_fwd": (
         _int,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int,

@@ -8,23 +8,14 @@
 // on the packed layout qkv[b][t][part][h*D + r], part 0/1/2 = q/k/v
 // (LiteLA.forward, :124-134), out[b][t][h*D + r].
 //
-// Pipeline (D = 32, bf16/f16 input):
-//   1. linattn_state_kernel   grid (ceil(H/2), splits, B): each workgroup streams
-//      one sequence split of two adjacent heads (128 contiguous bytes of K and of
-//      V per token) through LDS and accumulates S with v_mfma_f32_32x32x16; the
-//      token-major operands are read with ds_read_b64_tr_b16.  z accumulates on
-//      the VALU from the same registers.  Partials [B][H][splits][D+1][D] fp32.
-//   2. linattn_reduce_kernel  four state elements per thread: sums the partials
-//      in split order (fixed order: deterministic, no atomics).
-//   3. linattn_out_kernel     grid (ceil(H/4), ceil(N/64), B): one wavefront per
-//      head keeps S and z in registers as hi+lo 16-bit pairs (so the products
-//      carry ~16 mantissa bits of the fp32 state); relu(q) of 64 tokens x 4
-//      heads arrives with whole-line loads, is staged in LDS and read back as
-//      the B operand of v_mfma_f32_16x16x32; z is a third A operand whose rows
-//      all equal z, so the denominator lands in the same lanes as the
-//      numerator.  The normalised rows leave through LDS as whole-line stores.
-// Other head dims (128 % D == 0) and fp32 input take a VALU path with the same
-// three stages and the same fixed-order split reduction.
+// D = 32 with bf16/f16 input runs one fused kernel (linattn_fused_kernel):
+// each workgroup streams one sequence split of two adjacent heads, builds
+// the split's partial state on MFMA, waits at its (batch, head pair) group's
+// counter for the other splits, sums the group's partials in split order
+// (deterministic, no atomics on data) and contracts the state with the
+// split's relu(q) on MFMA.  Counters live in the workspace's control words.
+// Other head dims (128 % D == 0) and fp32 input take a VALU path in three
+// launches (split states, fixed-order split reduction, output).
 #include "kf_common.h"
 
 #include <mutex>
@@ -41,18 +32,40 @@ namespace {
 
 constexpr int kD = 32;              // head dim of the MFMA path
 constexpr int kState = (kD + 1) * kD;
-constexpr int kTT = 64;             // tokens per state tile
-constexpr int kRS = 72;             // LDS row stride (elements) of a 64-channel row
-constexpr int kOutTokens = 64;      // tokens per output workgroup
+constexpr int kTT = 128;            // tokens per tile (state and output phases)
+constexpr int kWaves = 8;           // wavefronts per fused workgroup: (head of the pair) x (32-token quarter)
+constexpr int kThreads = 64 * kWaves;
+// Tiles held in registers (in flight) per thread: three of each.  Deeper
+// rings (4-7) ran 2-20% slower on MI355X, as did 16-wave workgroups and
+// wave-private pipelines without the per-tile barrier.
+constexpr int KV_RING = 3;
+constexpr int Q_RING = 3;
+constexpr int kOutTokens = 64;      // tokens per output workgroup of the generic path
+constexpr int kSpinLimit = 1 << 20; // polls of the group counter before giving up
 
 // --------------------------------------------------------------------------
-// 1. Split-state producer (MFMA).
+// Control words at the start of the workspace (uint32):
+//   [0]          ticket counter (start order of the fused kernel's workgroups)
+//   [1]          error word: 1 = a group barrier timed out, 2 = a ticket beyond
+//                the grid (control words not zero on entry)
+//   [64 + 64g]   arrivals of group g (one (batch, head pair)) at its barrier
+//   [64 + 64g+1] departures of group g from it (each group's words share no
+//                cache line with another group's, so polls do not collide)
+// The region has a fixed size (kCtrlBytes), so a workspace reused for other
+// shapes keeps its control words apart from its partials.  They must be zero
+// before the first call; every call returns them to zero.
 // --------------------------------------------------------------------------
+constexpr int kCtrlHeader = 64;
+constexpr int kCtrlStride = 64;            // words per group: each group's counters own a 256-byte line
+constexpr int kMaxGroupsPerLaunch = 4096;  // larger problems take several launches
+constexpr int64_t kCtrlBytes = (int64_t)(kCtrlHeader + kCtrlStride * kMaxGroupsPerLaunch) * 4;
+static_assert(kCtrlBytes % 256 == 0, "partials stay 256-byte aligned");
+
 // Workgroup barrier that leaves global loads in flight.  __syncthreads()
 // also waits for every outstanding global load (vmcnt(0)), which would drain
-// the register prefetch below at each tile; here only this wave's LDS
-// traffic is completed (lgkmcnt(0)) before s_barrier.  The empty asm
-// statements keep the compiler from moving memory accesses across it.
+// the register prefetch at each tile; here only this wave's LDS traffic is
+// completed (lgkmcnt(0)) before s_barrier.  The empty asm statements keep
+// the compiler from moving memory accesses across it.
 __device__ __forceinline__ void barrier_keep_loads() {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt untouched
     asm volatile("" ::: "memory");
@@ -60,20 +73,56 @@ __device__ __forceinline__ void barrier_keep_loads() {
     asm volatile("" ::: "memory");
 }
 
-// Global -> register staging of one 64-token tile of a head pair: 4 x 16 B per
-// thread.  Chunk c = i*256 + tid: token c/16, part (c/8)%2 (0 = K, 1 = V),
-// 16-byte segment c%8 of the 128-byte two-head span, so every load
-// instruction of a wave covers 4 tokens x 2 whole 128-byte lines.  Addresses
-// are clamped into the split (token t_end-1) and onto the present head, so
-// the number of loads never depends on the data; the clamped duplicates are
-// zeroed when the tile is stored to LDS.
+// LDS byte offsets.  K/V tile: one 256-byte row per token holding the pair's
+// 64 K channels and 64 V channels; odd rows swap the K and V halves and rows
+// with bit 1 set swap the two 64-byte quarters of each half (16-byte chunk
+// index xor 4).  A 16-lane store group (one token's K and V) and a 32-lane
+// transposing read (4 consecutive tokens x 64 bytes) then touch 64 distinct
+// banks.
+__device__ __forceinline__ int kv_off(int tok, int part, int ch) {
+    return tok * 256 + ((part ^ (tok & 1)) << 7) + (((ch >> 3) ^ (((tok >> 1) & 1) << 2)) << 4) + (ch & 7) * 2;
+}
+// q and 16-bit output tiles: 128-byte rows (the pair's 64 channels), 16-byte
+// chunk index xor (row >> 1) & 7, so 16 consecutive rows at one chunk (an
+// MFMA operand read) hit 16 distinct slots, as do 2 rows x 8 chunks (a
+// whole-line staging access).
+__device__ __forceinline__ int r128_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+// fp32 output tile: 256-byte rows, chunk index xor (row & 15).
+__device__ __forceinline__ int r256_off(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
+
+template <typename TO> struct OutTile {
+    static constexpr int ROW = 2 * kD * (int)sizeof(TO);   // bytes per token row of the pair
+    static constexpr int CHUNKS = ROW / 16;
+    __device__ static int off(int row, int chunk) {
+        if constexpr (ROW == 128) return r128_off(row, chunk);
+        else return r256_off(row, chunk);
+    }
+};
+
+struct FusedParams {
+    const void* qkv;
+    void* out;
+    float* partial;     // [B][H][S][D+1][D]
+    unsigned* ctrl;
+    int N, H, npairs, S, split_len;
+    int g0;             // first group (batch * npairs + pair) of this launch
+    int total;          // workgroups of this launch: groups * S
+    float eps;
+};
+
+// Global -> register staging of one 128-token K/V tile of a head pair: 4 x 16 B
+// per thread.  Chunk c = i*512 + tid: token c/16, part (c/8)%2 (0 = K, 1 = V),
+// 16-byte segment c%8 of the pair's 128-byte span, so every load instruction
+// of a wave covers 4 tokens x 2 whole 128-byte lines.  Addresses are clamped
+// into the split (token t_end-1) and onto a present head, so the number of
+// loads never depends on the data; the clamped duplicates are zeroed when the
+// tile is stored to LDS.
 template <typename T>
-__device__ __forceinline__ void state_gload(u32x4 (&reg)[4], const T* __restrict__ qkv, int64_t b,
-                                            int N, int64_t C, int h0, int nh, int t0, int t_end,
-                                            int tid) {
+__device__ __forceinline__ void kv_gload(u32x4 (&reg)[4], const T* __restrict__ qkv, int64_t b, int N,
+                                         int64_t C, int h0, int nh, int t0, int t_end, int tid) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int c = i * 256 + tid;
+        const int c = i * kThreads + tid;
         const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
         const int t = min(t0 + tok, t_end - 1);
         const int sg = seg < nh * 4 ? seg : seg - 4;
@@ -82,55 +131,172 @@ __device__ __forceinline__ void state_gload(u32x4 (&reg)[4], const T* __restrict
     }
 }
 
+// One 128-token q tile of the pair: 2 x 16 B per thread, chunk c = i*512+tid:
+// token c/8, segment c%8 (whole 128-byte lines), clamped like kv_gload.
 template <typename T>
-__global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict__ qkv,
-                                                            float* __restrict__ partial, int N,
-                                                            int H, int split_len, int splits) {
-    // Head pairs vary fastest over the grid, so the workgroups resident at one
-    // time read neighbouring 128-byte spans of the same token rows.
-    const int g = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t C = (int64_t)H * kD;
-    const int h0 = 2 * g;
-    const int nh = min(2, H - h0);
-    const int t_begin = s * split_len;            // < N: the host sizes the grid
-    const int t_end = min(N, t_begin + split_len);
+__device__ __forceinline__ void q_gload(u32x4 (&reg)[2], const T* __restrict__ qkv, int64_t b, int N,
+                                        int64_t C, int h0, int nh, int t0, int t_end, int tid) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = i * kThreads + tid;
+        const int tok = c >> 3, seg = c & 7;
+        const int t = min(t0 + tok, t_end - 1);
+        const int sg = seg < nh * 4 ? seg : seg - 4;
+        const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (int64_t)h0 * kD + sg * 8;
+        reg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+    }
+}
 
-    // [buf][K,V][tok*kRS+ch]; after the scan the same memory combines the
-    // two token halves ([head slot][lane][16 accumulators + z]).
-    __shared__ __attribute__((aligned(16))) T tile[2][2][kTT * kRS];
-    static_assert(sizeof(tile) >= 2 * 64 * 17 * sizeof(float), "combine buffer fits in the tiles");
-    float (*comb)[64][17] = reinterpret_cast<float (*)[64][17]>(&tile[0][0][0]);
-
-    // Tile rows at or past t_end are stored as zeros; ReLU is applied to K.
-    auto lstore = [&](const u32x4 (&reg)[4], int buf, int t0) {
+// Stores of the numerator pair (n0: channels 4kg..4kg+3, n1: 16+4kg..) after
+// v_permlane16_swap has exchanged n1 of the even 16-lane groups with n0 of
+// the odd ones: an even group then holds channels 4kg..4kg+7, an odd group
+// 16+4(kg-1)..16+4(kg-1)+7, so each lane writes 8 consecutive channels.
+template <typename TO>
+__device__ __forceinline__ void store8_lds(unsigned char* tile, int row, int ch0, f32x4 a, f32x4 b) {
+    if constexpr (sizeof(TO) == 4) {
+        *reinterpret_cast<f32x4*>(tile + OutTile<TO>::off(row, ch0 / 4)) = a;
+        *reinterpret_cast<f32x4*>(tile + OutTile<TO>::off(row, ch0 / 4 + 1)) = b;
+    } else {
+        typename V<TO>::x8 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int c = i * 256 + tid;
-            const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
-            const u32x4 z = {0u, 0u, 0u, 0u};
-            const u32x4 v = t0 + tok < t_end ? (part == 0 ? relu_packed16(reg[i]) : reg[i]) : z;
-            *reinterpret_cast<u32x4*>(&tile[buf][part][tok * kRS + seg * 8]) = v;
+            o[i] = (TO)a[i];
+            o[i + 4] = (TO)b[i];
         }
-    };
+        *reinterpret_cast<typename V<TO>::x8*>(tile + OutTile<TO>::off(row, ch0 / 8)) = o;
+    }
+}
 
-    // Wave (hw, th): head slot hw, token half th of each 64-token tile.
+// Barrier of the workgroups of one group (the `members` sequence splits of one
+// (batch, head pair)): every writer's partial has completed at the device
+// coherence point (device-coherent stores, then a wait for them) before the
+// workgroup barrier that precedes this call; thread 0 counts the arrival,
+// polls until all members have arrived (at most kSpinLimit polls, then it
+// sets the error word and goes on, so no wave can wait forever), counts the
+// departure, and the last member to leave resets both counters to zero for
+// the next call.  The members then read the partials with plain loads (see
+// phase 2 for why they are current).  Agent-scope fences are not used: their L2 write-backs and
+// invalidations, once per workgroup, cost more than the rest of the kernel
+// on MI355X (write-backs ~67 us, invalidations ~10 us of a 37 us launch at
+// B=2, H=70, N=4096).
+__device__ __forceinline__ void group_barrier(unsigned* ctrl, int g, unsigned members) {
+    if (threadIdx.x == 0) {
+        unsigned* arrive = ctrl + kCtrlHeader + kCtrlStride * g;
+        unsigned* depart = arrive + 1;
+        __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int polls = 0;
+        while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < members) {
+            if (++polls > kSpinLimit) {
+                __hip_atomic_store(ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        if (__hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1) {
+            __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+}
+
+// --------------------------------------------------------------------------
+// The fused kernel (D = 32, 16-bit input).  One workgroup per (batch, head
+// pair, sequence split), numbered by a ticket taken at start, so the members
+// of a group start consecutively: a member can only wait for members that
+// started before it or will start next, and at most one group is partly
+// started at any time (its waiting members hold fewer slots than one XCD
+// has), so every wait ends.
+//   Phase 1: stream the split's K and V (three 128-token tiles in flight in
+//            registers, LDS double buffer), accumulate the partial state
+//            S = V^T relu(K) with v_mfma_f32_32x32x16 and z = sum relu(K),
+//            write it to the workspace.
+//   Barrier: wait for the group's other splits.
+//   Phase 2: sum the group's partials in split order (fixed order: the same
+//            state in every member, deterministic), then stream the split's
+//            q tiles: out = S relu(q) / (z . relu(q) + eps) on
+//            v_mfma_f32_16x16x32 with S and z held as hi+lo 16-bit pairs,
+//            rows leaving through LDS as whole-line stores.
+// Waves: (hw, th) = (head of the pair, 32-token quarter of each tile).
+// Where the time goes (MI355X, B=2, H=70, N=4096, 3 splits): phase 1 alone
+// ~19 us, phase 2 alone ~22 us, the two overlapping to ~33 us.  Phase 2 is
+// a mixed read/write stream of 128-byte spans; a probe of that traffic
+// alone reached ~4.2 TB/s at one 512-thread workgroup per CU.
+// --------------------------------------------------------------------------
+template <typename T, typename TO>
+__global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) {
+    constexpr int KV_BYTES = 2 * kTT * 256;                          // double-buffered K/V tile
+    constexpr int Q_BYTES = kTT * 128;
+    constexpr int O_BYTES = kTT * OutTile<TO>::ROW;
+    constexpr int P2_BYTES = 2 * (Q_BYTES + O_BYTES);                // double-buffered q and out tiles
+    constexpr int LDS_BYTES = KV_BYTES > P2_BYTES ? KV_BYTES : P2_BYTES;
+    static_assert(LDS_BYTES >= 2 * 3 * 64 * 17 * 4, "combine buffer fits");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+    __shared__ int sh_ticket;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        const int t = (int)__hip_atomic_fetch_add(p.ctrl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == p.total - 1) __hip_atomic_store(p.ctrl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sh_ticket = t;
+    }
+    __syncthreads();
+    const int ticket = sh_ticket;
+    if (ticket >= p.total) {
+        // Control words that were not zero on entry: flag it and touch nothing
+        // (the group barriers of the other workgroups then time out).
+        if (tid == 0) __hip_atomic_store(p.ctrl + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    const int g = ticket / p.S, s = ticket - g * p.S;  // group within this launch, split
+    const int gg = p.g0 + g;
+    const int b = gg / p.npairs, pair = gg - b * p.npairs;
+    const T* __restrict__ qkv = static_cast<const T*>(p.qkv);
+    const int N = p.N, H = p.H;
+    const int64_t C = (int64_t)H * kD;
+    const int h0 = 2 * pair;
+    const int nh = min(2, H - h0);
+    const int t_begin = s * p.split_len;          // < N: the host sizes the splits
+    const int t_end = min(N, t_begin + p.split_len);
+    const int ntile = (t_end - t_begin + kTT - 1) / kTT;  // >= 1
     const int hw = wave & 1, th = wave >> 1;
     const int G = lane >> 4, j16 = lane & 15;
+
+    // ---------------- Phase 1: partial state of this split ----------------
+    // ReLU on K only and zeros past t_end, as masks (no divergent branches).
+    const unsigned sign_bits = ((tid >> 3) & 1) ? 0u : 0x00010001u;  // part = (c/8)%2 = (tid/8)%2
+    auto kv_store = [&](const u32x4 (&reg)[4], int buf, int t0) {
+        unsigned char* base = lds + buf * (kTT * 256);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = i * kThreads + tid;
+            const int tok = c >> 4, part = (c >> 3) & 1, seg = c & 7;
+            const unsigned keep = t0 + tok < t_end ? 0xffffffffu : 0u;
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const unsigned neg = (reg[i][e] >> 15) & sign_bits;
+                v[e] = reg[i][e] & ~(neg * 0xffffu) & keep;
+            }
+            *reinterpret_cast<u32x4*>(base + kv_off(tok, part, seg * 8)) = v;
+        }
+    };
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = 0.f;
     float zsum = 0.f;
-
-    auto compute = [&](int buf) {
+    auto accumulate = [&](int buf) {
+        const unsigned char* base = lds + buf * (kTT * 256);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int row = 32 * th + 16 * ks + 8 * (G >> 1) + (j16 >> 2);
             const int col = hw * 32 + 16 * (G & 1) + 4 * (j16 & 3);
-            const T* vb = &tile[buf][1][row * kRS + col];
-            const T* kb = &tile[buf][0][row * kRS + col];
-            typename V<T>::x4 a0 = lds_read_tr(vb), a1 = lds_read_tr(vb + 4 * kRS);
-            typename V<T>::x4 b0 = lds_read_tr(kb), b1 = lds_read_tr(kb + 4 * kRS);
+            const T* v0 = reinterpret_cast<const T*>(base + kv_off(row, 1, col));
+            const T* v1 = reinterpret_cast<const T*>(base + kv_off(row + 4, 1, col));
+            const T* k0 = reinterpret_cast<const T*>(base + kv_off(row, 0, col));
+            const T* k1 = reinterpret_cast<const T*>(base + kv_off(row + 4, 0, col));
+            typename V<T>::x4 a0 = lds_read_tr(v0), a1 = lds_read_tr(v1);
+            typename V<T>::x4 b0 = lds_read_tr(k0), b1 = lds_read_tr(k1);
             typename V<T>::x8 a, bk;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -144,62 +310,240 @@ __global__ __launch_bounds__(256) void linattn_state_kernel(const T* __restrict_
             for (int j = 0; j < 8; ++j) zsum += (float)bk[j];
         }
     };
-
-    // Three tiles stay in flight in registers while one is consumed from LDS.
-    // Tile j is loaded into register set j % 3 and stored to LDS buffer j % 2
-    // one iteration ahead of its use.  The register set is chosen at compile
-    // time (the loop is unrolled by three), and every step issues its loads
-    // (past the end of the split they re-read row t_end-1), so the compiler's
-    // wait before each LDS store is an exact count of younger loads.
-    const int ntile = (t_end - t_begin + kTT - 1) / kTT;  // >= 1
-    u32x4 r0[4], r1[4], r2[4];
-    state_gload<T>(r0, qkv, b, N, C, h0, nh, t_begin, t_end, tid);
-    state_gload<T>(r1, qkv, b, N, C, h0, nh, t_begin + kTT, t_end, tid);
-    state_gload<T>(r2, qkv, b, N, C, h0, nh, t_begin + 2 * kTT, t_end, tid);
-    lstore(r0, 0, t_begin);
-    barrier_keep_loads();
-    // Step it: LDS buffer it&1 holds tile it; `nx` holds tile it+1; `fr` is
-    // free and receives tile it+3.
-    auto step = [&](int it, u32x4 (&fr)[4], u32x4 (&nx)[4]) {
-        state_gload<T>(fr, qkv, b, N, C, h0, nh, t_begin + (it + 3) * kTT, t_end, tid);
-        compute(it & 1);
-        lstore(nx, (it + 1) & 1, t_begin + (it + 1) * kTT);
-        barrier_keep_loads();
-    };
-    for (int it = 0; it < ntile; it += 3) {
-        step(it, r0, r1);
-        if (it + 1 < ntile) step(it + 1, r1, r2);
-        if (it + 2 < ntile) step(it + 2, r2, r0);
-    }
-
-    // Combine the two token halves of each head, then write the partial.
-    __syncthreads();
-    if (th == 1) {
+    {
+        // Tile j is loaded into register set j % KV_RING and stored to LDS
+        // buffer j % 2 one step ahead of its use, so KV_RING - 1 tiles are in
+        // flight while a step waits for the next one.  The register set is
+        // chosen at compile time (the loop body is KV_RING steps, unrolled),
+        // and every step issues its loads (past the end they re-read row
+        // t_end-1), so the compiler's wait before each LDS store is an exact
+        // count.
+        u32x4 ring[KV_RING][4];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) comb[hw][lane][i] = acc[i];
-        comb[hw][lane][16] = zsum;
+        for (int j = 0; j < KV_RING; ++j) kv_gload<T>(ring[j], qkv, b, N, C, h0, nh, t_begin + j * kTT, t_end, tid);
+        kv_store(ring[0], 0, t_begin);
+        barrier_keep_loads();
+        // Step it: LDS buffer it&1 holds tile it; ring[(it+1) % KV_RING] holds
+        // tile it+1; ring[it % KV_RING] is free and receives tile it+KV_RING.
+        auto step = [&](int it, u32x4 (&fr)[4], u32x4 (&nx)[4]) {
+            kv_gload<T>(fr, qkv, b, N, C, h0, nh, t_begin + (it + KV_RING) * kTT, t_end, tid);
+            accumulate(it & 1);
+            kv_store(nx, (it + 1) & 1, t_begin + (it + 1) * kTT);
+            barrier_keep_loads();
+        };
+        // Whole rounds of KV_RING steps in the loop, the remainder after it,
+        // so the loop's back edge always follows a full round.
+        int it = 0;
+        for (; it + KV_RING <= ntile; it += KV_RING) {
+#pragma unroll
+            for (int r = 0; r < KV_RING; ++r) step(it + r, ring[r], ring[(r + 1) % KV_RING]);
+        }
+#pragma unroll
+        for (int r = 0; r < KV_RING - 1; ++r)
+            if (it + r < ntile) step(it + r, ring[r], ring[(r + 1) % KV_RING]);
+    }
+    // Combine the four token quarters of each head (in quarter order), then
+    // write the partial.
+    __syncthreads();
+    float (*comb)[3][64][17] = reinterpret_cast<float (*)[3][64][17]>(lds);
+    if (th > 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) comb[hw][th - 1][lane][i] = acc[i];
+        comb[hw][th - 1][lane][16] = zsum;
     }
     __syncthreads();
     if (th == 0) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] += comb[hw][lane][i];
-        zsum += comb[hw][lane][16];
+        for (int q = 0; q < 3; ++q) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] += comb[hw][q][lane][i];
+            zsum += comb[hw][q][lane][16];
+        }
         zsum += __shfl_xor(zsum, 32, 64);  // lanes l and l+32 hold the same channel
         if (hw < nh) {
-            float* P = partial + ((int64_t)(b * H + h0 + hw) * splits + s) * kState;
+            // Device-coherent stores (sc1: written through to the coherence
+            // point shared by all XCDs), so no L2 write-back is needed before
+            // the other members read them.
+            float* P = p.partial + ((int64_t)(b * H + h0 + hw) * p.S + s) * kState;
             const int c = lane & 31;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int r = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                P[r * kD + c] = acc[i];
+                __hip_atomic_store(P + r * kD + c, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            if (lane < 32) P[kD * kD + c] = zsum;
+            if (lane < 32) __hip_atomic_store(P + kD * kD + c, zsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // The stores have completed at the coherence point before this wave
+        // reaches the workgroup barrier that precedes the arrival count.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+
+    // The first Q_RING q tiles are requested before the barrier, so their
+    // latency overlaps the wait for the other splits.
+    u32x4 qring[Q_RING][2];
+#pragma unroll
+    for (int j = 0; j < Q_RING; ++j) q_gload<T>(qring[j], qkv, b, N, C, h0, nh, t_begin + j * kTT, t_end, tid);
+    barrier_keep_loads();
+    group_barrier(p.ctrl, g, (unsigned)p.S);
+
+    // ---------------- Phase 2: the group's state, then the outputs --------
+    // The group's partials of both heads (2 x 1056 floats, 528 16-byte
+    // vectors) are summed in split order by all 512 threads into LDS (inside
+    // the first out buffer, which is first written after the phase-2 loop's
+    // first barrier, when every wave has read its state), eight splits' loads
+    // in flight at a time.  Plain loads
+    // see the partials: they were written with device-coherent stores that
+    // completed before their writers arrived, and no cache holds a line of
+    // them from before the barrier (nothing reads them earlier in a launch,
+    // and caches start every launch invalidated).
+    float* sums = reinterpret_cast<float*>(lds + 2 * Q_BYTES);
+    static_assert(2 * Q_BYTES + 2 * kState * 4 <= LDS_BYTES, "state sums fit");
+    {
+        constexpr int NV = 2 * kState / 4;  // 16-byte vectors of the pair's state
+        const float* P0 = p.partial + (int64_t)(b * H + h0) * p.S * kState;
+        const float* P1 = nh > 1 ? P0 + (int64_t)p.S * kState : P0;
+        for (int v = tid; v < NV; v += kThreads) {
+            const int e = 4 * v;
+            const float* P = e < kState ? P0 + e : P1 + (e - kState);
+            f32x4 acc4 = {0.f, 0.f, 0.f, 0.f};
+            for (int s0 = 0; s0 < p.S; s0 += 8) {
+                f32x4 part4[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    part4[j] = s0 + j < p.S ? *reinterpret_cast<const f32x4*>(P + (int64_t)(s0 + j) * kState)
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc4 += part4[j];  // split order; padding adds zero
+            }
+            *reinterpret_cast<f32x4*>(sums + e) = acc4;
         }
     }
+    barrier_keep_loads();
+    // S and z of head hw as hi+lo 16-bit A operands: rows r = 16*mb + m16,
+    // k = c = 8*kg + j; the third operand repeats z on every row, so the
+    // denominator lands in the same lanes as the numerator.
+    const int m16 = lane & 15, kg = lane >> 4;
+    float sv[2][8], zv[8];
+    {
+        const float* S0 = sums + hw * kState;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            sv[0][j] = S0[m16 * kD + 8 * kg + j];
+            sv[1][j] = S0[(16 + m16) * kD + 8 * kg + j];
+            zv[j] = S0[kD * kD + 8 * kg + j];
+        }
+    }
+    // fp16 has a narrow exponent range: rescale the whole state by a power of
+    // two (out = num/den is invariant to a common factor; only eps sees it).
+    float scale = 1.f;
+    if constexpr (sizeof(T) == 2 && !__is_same(T, bf16)) {
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            mx = fmaxf(mx, fmaxf(fabsf(zv[j]), fmaxf(fabsf(sv[0][j]), fabsf(sv[1][j]))));
+        mx = wave_max(mx);
+        if (mx > 0.f) {
+            int e;
+            frexpf(mx, &e);
+            scale = ldexpf(1.f, -e);
+        }
+    }
+    typename V<T>::x8 shi[2], slo[2], zhi, zlo;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+            const float x = sv[mb][j] * scale;
+            const T hi = (T)x;
+            shi[mb][j] = hi;
+            slo[mb][j] = (T)(x - (float)hi);
+        }
+        const float x = zv[j] * scale;
+        const T hi = (T)x;
+        zhi[j] = hi;
+        zlo[j] = (T)(x - (float)hi);
+    }
+    const float eps = p.eps * scale;
+
+    TO* __restrict__ out = static_cast<TO*>(p.out);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    const int ch0 = (kg & 1) ? 16 + 4 * (kg - 1) : 4 * kg;  // first channel a lane stores
+    constexpr int OCH = OutTile<TO>::CHUNKS;                  // 16-byte chunks per token row
+    constexpr int OROUNDS = kTT * OCH / kThreads;             // store rounds per tile
+    const int valid_chunks = nh * OCH / 2;
+    auto qbuf = [&](int i) { return lds + (i & 1) * Q_BYTES; };
+    auto obuf = [&](int i) { return lds + 2 * Q_BYTES + (i & 1) * O_BYTES; };
+    auto q_store = [&](const u32x4 (&reg)[2], int i) {
+        unsigned char* base = qbuf(i);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int c = k * kThreads + tid;
+            *reinterpret_cast<u32x4*>(base + r128_off(c >> 3, c & 7)) = relu_packed16(reg[k]);
+        }
+    };
+    auto out_tile = [&](int i) {
+        const unsigned char* qb = qbuf(i);
+        unsigned char* ob = obuf(i);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int row = 32 * th + 16 * u + m16;
+            const typename V<T>::x8 bq = *reinterpret_cast<const typename V<T>::x8*>(qb + r128_off(row, 4 * hw + kg));
+            f32x4 n0 = mfma16x16x32(shi[0], bq, zero);
+            n0 = mfma16x16x32(slo[0], bq, n0);
+            f32x4 n1 = mfma16x16x32(shi[1], bq, zero);
+            n1 = mfma16x16x32(slo[1], bq, n1);
+            f32x4 dn = mfma16x16x32(zhi, bq, zero);
+            dn = mfma16x16x32(zlo, bq, dn);
+            const float inv = 1.0f / (dn[0] + eps);
+            f32x4 lo, hi;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(n0[k] * inv),
+                                                                __float_as_uint(n1[k] * inv), false, false);
+                lo[k] = __uint_as_float(r[0]);
+                hi[k] = __uint_as_float(r[1]);
+            }
+            store8_lds<TO>(ob, row, hw * kD + ch0, lo, hi);
+        }
+    };
+    auto out_store = [&](int i, int t0) {
+        const unsigned char* ob = obuf(i);
+#pragma unroll
+        for (int k = 0; k < OROUNDS; ++k) {
+            const int c = k * kThreads + tid;
+            const int tok = c / OCH, chunk = c % OCH;
+            if (t0 + tok < t_end && chunk < valid_chunks) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(ob + OutTile<TO>::off(tok, chunk));
+                unsigned char* dst = reinterpret_cast<unsigned char*>(out + ((int64_t)b * N + t0 + tok) * C +
+                                                                      (int64_t)h0 * kD);
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + chunk * 16));
+            }
+        }
+    };
+    // Tile i: q registers -> LDS q buffer i&1, barrier, MFMA -> LDS out buffer
+    // i&1, barrier, whole-line stores; the double buffers make two barriers
+    // per tile enough.  Q_RING q tiles stay in flight in registers.
+    auto pstep = [&](int it, u32x4 (&cur)[2]) {
+        const int t0 = t_begin + it * kTT;
+        q_store(cur, it);
+        q_gload<T>(cur, qkv, b, N, C, h0, nh, t0 + Q_RING * kTT, t_end, tid);
+        barrier_keep_loads();
+        out_tile(it);
+        barrier_keep_loads();
+        out_store(it, t0);
+    };
+    int it = 0;
+    for (; it + Q_RING <= ntile; it += Q_RING) {
+#pragma unroll
+        for (int r = 0; r < Q_RING; ++r) pstep(it + r, qring[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < Q_RING - 1; ++r)
+        if (it + r < ntile) pstep(it + r, qring[r]);
 }
 
 // --------------------------------------------------------------------------
-// 2. Fixed-order reduction of the split partials.
+// Fixed-order reduction of the split partials (generic path).
 // --------------------------------------------------------------------------
 // VEC consecutive state elements of one (batch, head) per thread; the
 // partials of all splits are loaded eight at a time (a short last batch is
@@ -244,167 +588,9 @@ int launch_reduce(const float* partial, float* state, int64_t n_heads, int split
     return check_launch("linattn_reduce_kernel launch");
 }
 
-// --------------------------------------------------------------------------
-// 3. Output contraction (MFMA, state in registers).
-// --------------------------------------------------------------------------
-// Stores of the numerator pair (n0: channels 4kg..4kg+3, n1: 16+4kg..) after
-// v_permlane16_swap has exchanged n1 of the even 16-lane groups with n0 of
-// the odd ones: an even group then holds channels 4kg..4kg+7, an odd group
-// 16+4(kg-1)..16+4(kg-1)+7, so each lane writes 8 consecutive channels.
-template <typename TO> struct Store8;
-template <> struct Store8<float> {
-    __device__ static void run(float* p, f32x4 a, f32x4 b) {
-        *reinterpret_cast<f32x4*>(p) = a;
-        *reinterpret_cast<f32x4*>(p + 4) = b;
-    }
-};
-template <typename TO> struct Store8 {
-    __device__ static void run(TO* p, f32x4 a, f32x4 b) {
-        typename V<TO>::x8 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[i] = (TO)a[i];
-            o[i + 4] = (TO)b[i];
-        }
-        *reinterpret_cast<typename V<TO>::x8*>(p) = o;
-    }
-};
-
-// Output workgroup: 4 wavefronts = 4 consecutive heads (one 256-byte span
-// of each token row) x kOutTokens tokens.  q arrives with whole-line loads
-// (each wave instruction: 4 tokens x 256 B) and is staged in LDS; each wave
-// then reads the MFMA B operand of its own head (16 tokens x 32 channels)
-// from LDS.  The normalised rows go back through LDS so that the stores are
-// whole lines too.  Loads and stores that split 128-byte lines between
-// wavefronts ran at ~60% of the whole-line rate on MI355X.
-template <typename T, typename TO>
-__global__ __launch_bounds__(256) void linattn_out_kernel(const T* __restrict__ qkv,
-                                                          const float* __restrict__ state,
-                                                          TO* __restrict__ out, int N, int H,
-                                                          float eps) {
-    constexpr int TT = kOutTokens;
-    constexpr int QR = 4 * kD + 8;            // q tile row stride (elements), padded
-    constexpr int OB = 4 * kD * sizeof(TO);   // output bytes per token row of 4 heads
-    constexpr int OR = OB + 16;               // out tile row stride (bytes), padded
-    __shared__ __attribute__((aligned(16))) T qt[TT * QR];
-    __shared__ __attribute__((aligned(16))) unsigned char ot[TT * OR];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int b = blockIdx.z;
-    const int hq0 = blockIdx.x * 4;           // head quads vary fastest over the grid
-    const int nhq = min(4, H - hq0);
-    const int h = hq0 + wave;
-    const int hs = h < H ? h : hq0;           // a missing head computes on head hq0, unstored
-    const int64_t C = (int64_t)H * kD;
-    const int m16 = lane & 15, kg = lane >> 4;
-    const int lr = lane >> 4, lc = lane & 15;  // whole-line load: token row lr, 16-byte chunk lc
-    const int lcc = lc < nhq * 4 ? lc : 0;
-
-    // S and z of this wave's head as hi+lo 16-bit A operands: rows
-    // r = 16*mb + m16, k = c = 8*kg + j; the third operand repeats z on every
-    // row, so the denominator lands in the same lanes as the numerator.
-    const float* S = state + (int64_t)(b * H + hs) * kState;
-    float sv[2][8], zv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        sv[0][j] = S[(m16)*kD + 8 * kg + j];
-        sv[1][j] = S[(16 + m16) * kD + 8 * kg + j];
-        zv[j] = S[kD * kD + 8 * kg + j];
-    }
-    // fp16 has a narrow exponent range: rescale the whole state by a power of
-    // two (out = num/den is invariant to a common factor; only eps sees it).
-    float scale = 1.f;
-    if constexpr (sizeof(T) == 2 && !__is_same(T, bf16)) {
-        float mx = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            mx = fmaxf(mx, fmaxf(fabsf(zv[j]), fmaxf(fabsf(sv[0][j]), fabsf(sv[1][j]))));
-        mx = wave_max(mx);
-        if (mx > 0.f) {
-            int e;
-            frexpf(mx, &e);
-            scale = ldexpf(1.f, -e);
-        }
-    }
-    typename V<T>::x8 shi[2], slo[2], zhi, zlo;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            const float x = sv[mb][j] * scale;
-            const T hi = (T)x;
-            shi[mb][j] = hi;
-            slo[mb][j] = (T)(x - (float)hi);
-        }
-        const float x = zv[j] * scale;
-        const T hi = (T)x;
-        zhi[j] = hi;
-        zlo[j] = (T)(x - (float)hi);
-    }
-
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    const int c0 = (kg & 1) ? 16 + 4 * (kg - 1) : 4 * kg;
-    constexpr int LPR = OB / 16;              // lanes per output row (16 bf16/f16, 32 fp32)
-    constexpr int RPI = 64 / LPR;             // output rows per store instruction
-    const int sr = lane / LPR, sc = lane % LPR;
-    const bool sc_ok = sc * 16 < nhq * kD * (int)sizeof(TO);
-
-    const int n_blocks = (N + TT - 1) / TT;
-    for (int tb = blockIdx.y; tb < n_blocks; tb += gridDim.y) {
-        const int t_block = tb * TT;
-        const int t_stop = min(N, t_block + TT);
-        // Rows past t_stop re-read row t_stop-1; their results are not stored.
-        u32x4 qv[TT / 16];
-#pragma unroll
-        for (int k = 0; k < TT / 16; ++k) {
-            const int t = min(t_block + 4 * (4 * k + wave) + lr, t_stop - 1);
-            const T* src = qkv + ((int64_t)b * N + t) * 3 * C + (int64_t)hq0 * kD + lcc * 8;
-            qv[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-        }
-        if (tb != blockIdx.y) __syncthreads();  // the previous block's LDS reads are done
-#pragma unroll
-        for (int k = 0; k < TT / 16; ++k) {
-            const int row = 4 * (4 * k + wave) + lr;
-            *reinterpret_cast<u32x4*>(&qt[row * QR + lc * 8]) = relu_packed16(qv[k]);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < TT / 16; ++u) {
-            const int row = 16 * u + m16;
-            const typename V<T>::x8 bq =
-                *reinterpret_cast<const typename V<T>::x8*>(&qt[row * QR + wave * kD + 8 * kg]);
-            f32x4 n0 = mfma16x16x32(shi[0], bq, zero);
-            n0 = mfma16x16x32(slo[0], bq, n0);
-            f32x4 n1 = mfma16x16x32(shi[1], bq, zero);
-            n1 = mfma16x16x32(slo[1], bq, n1);
-            f32x4 dn = mfma16x16x32(zhi, bq, zero);
-            dn = mfma16x16x32(zlo, bq, dn);
-            const float inv = 1.0f / (dn[0] + eps);
-            f32x4 lo, hi;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(n0[i] * inv),
-                                                                __float_as_uint(n1[i] * inv), false, false);
-                lo[i] = __uint_as_float(r[0]);
-                hi[i] = __uint_as_float(r[1]);
-            }
-            // Even groups now hold (n0 own, n0 of the odd partner) = channels
-            // 4kg..4kg+7; odd groups (n1 of the even partner, n1 own) = channels
-            // 16+4(kg-1)..16+4(kg-1)+7.
-            Store8<TO>::run(reinterpret_cast<TO*>(&ot[row * OR + (wave * kD + c0) * sizeof(TO)]), lo, hi);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < TT / (4 * RPI); ++k) {
-            const int row = RPI * (4 * k + wave) + sr;
-            const int t = t_block + row;
-            if (t < t_stop && sc_ok) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(&ot[row * OR + sc * 16]);
-                unsigned char* dst = reinterpret_cast<unsigned char*>(out + ((int64_t)b * N + t) * C + (int64_t)hq0 * kD);
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + sc * 16));
-            }
-        }
-    }
+// Zeroes n words (the control words of a fresh workspace).
+__global__ __launch_bounds__(256) void linattn_zero_kernel(unsigned* __restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
 }
 
 // --------------------------------------------------------------------------
@@ -514,37 +700,61 @@ int64_t split_len_for(int64_t N, int64_t splits, int64_t align) {
     return (len + align - 1) / align * align;
 }
 
+// Workspace regions: control words, split partials, reduced states (the
+// generic path's; the fused kernel keeps its state in registers).
+struct Workspace {
+    unsigned* ctrl;
+    float* partial;
+    float* state;
+};
+
 template <typename T, typename TO>
-int run_mfma(const void* qkv, void* out, float* partial, float* state, int B, int N, int H,
-             int splits, int split_len, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL((linattn_state_kernel<T>), dim3((H + 1) / 2, splits, B), dim3(256), 0,
-                       stream, static_cast<const T*>(qkv), partial, N, H, split_len, splits);
-    if (int rc = check_launch("linattn_state_kernel launch")) return rc;
-    if (int rc = launch_reduce(partial, state, (int64_t)B * H, splits, kState, stream)) return rc;
-    hipLaunchKernelGGL((linattn_out_kernel<T, TO>),
-                       dim3((H + 3) / 4, out_grid_y(N), B), dim3(256), 0,
-                       stream, static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);
-    return check_launch("linattn_out_kernel launch");
+int run_mfma(const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
+             int split_len, float eps, hipStream_t stream) {
+    FusedParams p;
+    p.qkv = qkv;
+    p.out = out;
+    p.partial = ws.partial;
+    p.ctrl = ws.ctrl;
+    p.N = N;
+    p.H = H;
+    p.npairs = (H + 1) / 2;
+    p.S = splits;
+    p.split_len = split_len;
+    p.eps = eps;
+    const int64_t groups = (int64_t)B * p.npairs;
+    // Groups per launch: the control region holds kMaxGroupsPerLaunch groups,
+    // and a launch's workgroup count stays below 2^31.
+    int64_t per = kMaxGroupsPerLaunch;
+    if (per * splits > 0x7fffffffLL) per = 0x7fffffffLL / splits;
+    for (int64_t g0 = 0; g0 < groups; g0 += per) {
+        const int64_t n = groups - g0 < per ? groups - g0 : per;
+        p.g0 = (int)g0;
+        p.total = (int)(n * splits);
+        hipLaunchKernelGGL((linattn_fused_kernel<T, TO>), dim3((unsigned)p.total), dim3(kThreads), 0, stream, p);
+        if (int rc = check_launch("linattn_fused_kernel launch")) return rc;
+    }
+    return KF_OK;
 }
 
 template <typename T, typename TO, int DG>
-int run_generic(const void* qkv, void* out, float* partial, float* state, int B, int N, int H,
-                int splits, int split_len, float eps, hipStream_t stream) {
+int run_generic(const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
+                int split_len, float eps, hipStream_t stream) {
     hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(H, splits, B), dim3(256), 0, stream,
-                       static_cast<const T*>(qkv), partial, N, H, split_len, splits);
+                       static_cast<const T*>(qkv), ws.partial, N, H, split_len, splits);
     if (int rc = check_launch("linattn_state_generic launch")) return rc;
-    if (int rc = launch_reduce(partial, state, (int64_t)B * H, splits, (DG + 1) * DG, stream)) return rc;
+    if (int rc = launch_reduce(ws.partial, ws.state, (int64_t)B * H, splits, (DG + 1) * DG, stream)) return rc;
     hipLaunchKernelGGL((linattn_out_generic<T, TO, DG>),
                        dim3(H, out_grid_y(N), B), dim3(256), 0, stream,
-                       static_cast<const T*>(qkv), state, static_cast<TO*>(out), N, H, eps);
+                       static_cast<const T*>(qkv), ws.state, static_cast<TO*>(out), N, H, eps);
     return check_launch("linattn_out_generic launch");
 }
 
 template <typename T, typename TO>
-int run_generic_d(int D, const void* qkv, void* out, float* partial, float* state, int B, int N,
-                  int H, int splits, int split_len, float eps, hipStream_t stream) {
+int run_generic_d(int D, const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
+                  int split_len, float eps, hipStream_t stream) {
 #define KF_GENERIC_CASE(DD) \
-    case DD: return run_generic<T, TO, DD>(qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
+    case DD: return run_generic<T, TO, DD>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
     switch (D) {
         KF_GENERIC_CASE(1) KF_GENERIC_CASE(2) KF_GENERIC_CASE(4) KF_GENERIC_CASE(8)
         KF_GENERIC_CASE(16) KF_GENERIC_CASE(32) KF_GENERIC_CASE(64) KF_GENERIC_CASE(128)
@@ -554,21 +764,21 @@ int run_generic_d(int D, const void* qkv, void* out, float* partial, float* stat
 }
 
 template <typename T>
-int run_in(int out_dt, bool mfma, int D, const void* qkv, void* out, float* partial, float* state,
-           int B, int N, int H, int splits, int split_len, float eps, hipStream_t stream) {
+int run_in(int out_dt, bool mfma, int D, const void* qkv, void* out, const Workspace& ws, int B, int N,
+           int H, int splits, int split_len, float eps, hipStream_t stream) {
     if (mfma) {
         if constexpr (sizeof(T) == 2) {
             switch (out_dt) {
-                case KF_F32: return run_mfma<T, float>(qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
-                case KF_F16: return run_mfma<T, f16>(qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
-                case KF_BF16: return run_mfma<T, bf16>(qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
+                case KF_F32: return run_mfma<T, float>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+                case KF_F16: return run_mfma<T, f16>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+                case KF_BF16: return run_mfma<T, bf16>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
             }
         }
     }
     switch (out_dt) {
-        case KF_F32: return run_generic_d<T, float>(D, qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
-        case KF_F16: return run_generic_d<T, f16>(D, qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
-        case KF_BF16: return run_generic_d<T, bf16>(D, qkv, out, partial, state, B, N, H, splits, split_len, eps, stream);
+        case KF_F32: return run_generic_d<T, float>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+        case KF_F16: return run_generic_d<T, f16>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+        case KF_BF16: return run_generic_d<T, bf16>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
     }
     set_error("linattn: unknown output dtype %d", out_dt);
     return KF_E_INVALID;
@@ -581,15 +791,23 @@ bool valid_dim(int64_t D) { return D > 0 && D <= 128 && 128 % D == 0; }
 
 extern "C" int64_t kf_linattn_default_splits(int64_t batch, int64_t heads, int64_t dim,
                                              int64_t seq_len) {
-    // Aim for about 1.75 state workgroups per CU, each streaming at least 64
-    // tokens (one tile) of a head pair.  A sweep of the whole pipeline on
-    // MI355X (B=2/N=4096 and B=1/N=16384, 70 heads) found its minimum at 1.6-1.9
-    // workgroups per CU: fewer, longer streams beat four short ones per CU by
-    // 4-7%, and fewer than one per CU leaves CUs idle.
+    // D = 32 (the fused kernel): one workgroup per CU at most, each streaming
+    // at least one 128-token tile of a head pair.  The members of a group meet
+    // at a barrier, so every member waits for the slowest: a grid that leaves
+    // some CUs with two workgroups and others with one ran 10-20% slower on
+    // MI355X than one workgroup per CU (B=2, H=70, N=4096: 36.3 us at 3 splits
+    // = 210 workgroups, 41.8 us at 4 = 280; B=1, N=16384: 57.6 us at 7 = 245,
+    // 74.1 us at 8 = 280).  Other head dims: about 1.75 workgroups per CU.
     if (batch <= 0 || heads <= 0 || seq_len <= 0) return 1;
-    const int64_t groups = dim == kf::kD ? batch * ((heads + 1) / 2) : batch * heads;
-    const int64_t target = (7 * (int64_t)kf::device_cu_count() + 3) / 4;
-    int64_t splits = (target + groups - 1) / groups;
+    const int64_t cus = kf::device_cu_count();
+    int64_t splits;
+    if (dim == kf::kD) {
+        const int64_t groups = batch * ((heads + 1) / 2);
+        splits = cus / groups;
+    } else {
+        const int64_t groups = batch * heads;
+        splits = ((7 * cus + 3) / 4 + groups - 1) / groups;
+    }
     const int64_t max_splits = (seq_len + kf::kTT - 1) / kf::kTT;
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
@@ -601,14 +819,25 @@ extern "C" int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int6
     if (batch <= 0 || heads <= 0 || !kf::valid_dim(dim)) return 0;
     if (splits < 1) splits = 1;
     const int64_t state = (dim + 1) * dim;
-    return (int64_t)sizeof(float) * batch * heads * state * (splits + 1);
+    return kf::kCtrlBytes + (int64_t)sizeof(float) * batch * heads * state * (splits + 1);
 }
 
 namespace kf {
 namespace {
 
-// Validates the request, resolves the split count and runs the three
-// stages with `workspace` holding the partials and the reduced states.
+// Zeroes the first `bytes` of a workspace (rounded down to whole words).
+int zero_words(void* ws, int64_t bytes, hipStream_t s) {
+    const int64_t n = bytes / 4;
+    if (n <= 0) return KF_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(linattn_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<unsigned*>(ws), n);
+    return check_launch("linattn_zero_kernel launch");
+}
+
+// Validates the request, resolves the split count and runs the kernels with
+// `workspace` holding the control words, the partials and (generic path)
+// the reduced states.
 int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_bytes, int64_t batch,
                 int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
                 int out_dtype, hipStream_t s) {
@@ -631,27 +860,32 @@ int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_b
     KF_REQUIRE(workspace && workspace_bytes >= need, KF_E_WORKSPACE,
                "linattn: workspace of %lld bytes needed, %lld given", (long long)need,
                (long long)workspace_bytes);
+    KF_REQUIRE((uintptr_t)workspace % 256 == 0, KF_E_WORKSPACE, "linattn: workspace must be 256-byte aligned");
     const bool mfma = dim == kD && in_dtype != KF_F32 && (uintptr_t)qkv % 16 == 0 &&
                       (uintptr_t)out % 16 == 0;
-    // The split index is the y grid dimension (at most 65535 blocks).
+    // The generic path's split index is a y grid dimension (at most 65535).
     const int64_t split_len = split_len_for(seq_len, splits < 65535 ? splits : 65535, mfma ? kTT : kGT);
     const int64_t eff_splits = (seq_len + split_len - 1) / split_len;
     KF_REQUIRE(eff_splits <= 65535, KF_E_UNSUPPORTED, "linattn: too many splits");
     const int64_t state_size = (dim + 1) * dim;
-    float* partial = static_cast<float*>(workspace);
-    float* state = partial + batch * heads * state_size * splits;
+    Workspace ws;
+    ws.ctrl = static_cast<unsigned*>(workspace);
+    ws.partial = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kCtrlBytes);
+    ws.state = ws.partial + batch * heads * state_size * splits;
     const int B = (int)batch, N = (int)seq_len, H = (int)heads, D = (int)dim;
     const int S = (int)eff_splits, L = (int)split_len;
     switch (in_dtype) {
-        case KF_BF16: return run_in<bf16>(out_dtype, mfma, D, qkv, out, partial, state, B, N, H, S, L, eps, s);
-        case KF_F16: return run_in<f16>(out_dtype, mfma, D, qkv, out, partial, state, B, N, H, S, L, eps, s);
-        default: return run_in<float>(out_dtype, false, D, qkv, out, partial, state, B, N, H, S, L, eps, s);
+        case KF_BF16: return run_in<bf16>(out_dtype, mfma, D, qkv, out, ws, B, N, H, S, L, eps, s);
+        case KF_F16: return run_in<f16>(out_dtype, mfma, D, qkv, out, ws, B, N, H, S, L, eps, s);
+        default: return run_in<float>(out_dtype, false, D, qkv, out, ws, B, N, H, S, L, eps, s);
     }
 }
 
 // Per-device address of `scratch`, resolved once per device with that
-// device current (each GPU holds its own copy at its own address).
-int scratch_for_current_device(void** ptr) {
+// device current (each GPU holds its own copy at its own address).  The
+// first call on a device also zeroes the scratch's control words on the
+// caller's stream (the array starts zeroed at load; this makes it explicit).
+int scratch_for_current_device(void** ptr, hipStream_t stream) {
     static std::mutex lock;
     static void* addr[64] = {};
     int dev = 0;
@@ -663,6 +897,7 @@ int scratch_for_current_device(void** ptr) {
         void* p = nullptr;
         err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (err != hipSuccess) return hip_failure(err, "linattn: hipGetSymbolAddress(scratch)");
+        if (int rc = zero_words(p, kCtrlBytes, stream)) return rc;
         addr[dev] = p;
     }
     *ptr = addr[dev];
@@ -671,6 +906,14 @@ int scratch_for_current_device(void** ptr) {
 
 }  // namespace
 }  // namespace kf
+
+extern "C" int kf_linattn_workspace_init(void* workspace, int64_t workspace_bytes, kf_stream_t stream) {
+    using namespace kf;
+    KF_REQUIRE(workspace_bytes >= 0, KF_E_INVALID, "linattn: negative workspace size");
+    KF_REQUIRE(workspace || workspace_bytes == 0, KF_E_INVALID, "linattn: null workspace");
+    const int64_t n = workspace_bytes < kCtrlBytes ? workspace_bytes : kCtrlBytes;
+    return zero_words(workspace, n, static_cast<hipStream_t>(stream));
+}
 
 extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64_t workspace_bytes,
                               int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
@@ -699,7 +942,7 @@ extern "C" int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch,
         return linattn_run(qkv, out, nullptr, 0, batch, seq_len, heads, dim, eff, eps, in_dtype, out_dtype,
                            static_cast<hipStream_t>(stream));
     void* ws = nullptr;
-    if (int rc = scratch_for_current_device(&ws)) return rc;
+    if (int rc = scratch_for_current_device(&ws, static_cast<hipStream_t>(stream))) return rc;
     return linattn_run(qkv, out, ws, kLinattnScratchBytes, batch, seq_len, heads, dim, eff, eps, in_dtype,
                        out_dtype, static_cast<hipStream_t>(stream));
 }

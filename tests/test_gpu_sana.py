@@ -118,23 +118,56 @@ def test_validation_and_splits():
 
 
 @pytest.mark.parametrize("dim", [32, 16])
-def test_unaligned_workspace_matches_aligned(dim):
-    """The split reduction reads 16-byte vectors only from an aligned
-    workspace; a workspace 4 bytes off takes the scalar reduction, which sums
-    in the same split order and so gives the same bits."""
+def test_workspace_contract(dim):
+    """A workspace is zeroed once (kf_linattn_workspace_init) and then serves
+    calls of any shape it is large enough for: every call leaves its control
+    words (the fused kernel's group counters) zero, and the error word that a
+    timed-out group barrier would set stays zero.  An unaligned workspace is
+    refused on the host."""
     from kernelforge_amd import _lib
 
     lib = _lib.load()
-    H, N, splits = 256 // dim, 1000, 13
-    qkv = randn((2, N, 3, H * dim), torch.bfloat16, seed=5).to(DEV)
-    need = int(lib.kf_linattn_workspace_bytes(2, H, dim, splits))
-    ws = torch.empty(need + 64, device=DEV, dtype=torch.uint8)
-    outs = []
-    for off in (0, 4):
-        out = torch.empty(2, N, H * dim, device=DEV, dtype=torch.float32)
-        rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), ctypes.c_void_p(ws.data_ptr() + off), need, 2, N, H,
-                                dim, splits, 1e-15, _lib.KF_BF16, _lib.KF_F32, _lib.stream_of(qkv))
-        _lib.check(rc, "kf_linattn_fwd")
-        outs.append(out)
-    assert torch.equal(outs[0], outs[1])
-    check(outs[0], orc.linear_attention(qkv.cpu(), H, dim), 1e-4)
+    H = 256 // dim
+    big = int(lib.kf_linattn_workspace_bytes(2, 16, dim, 13))
+    ws = torch.empty(big + 256, device=DEV, dtype=torch.uint8)
+    stream = _lib.stream_of(ws)
+    _lib.check(lib.kf_linattn_workspace_init(_lib.ptr(ws), big, stream), "kf_linattn_workspace_init")
+    for B, N, heads, splits in ((2, 1000, H, 13), (1, 333, 3, 5), (2, 4096, 16, 7), (1, 64, H, 1)):
+        qkv = randn((B, N, 3, heads * dim), torch.bfloat16, seed=N).to(DEV)
+        out = torch.empty(B, N, heads * dim, device=DEV, dtype=torch.float32)
+        need = int(lib.kf_linattn_workspace_bytes(B, heads, dim, splits))
+        assert need <= big
+        for _ in range(2):
+            rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), _lib.ptr(ws), big, B, N, heads, dim, splits,
+                                    1e-15, _lib.KF_BF16, _lib.KF_F32, stream)
+            _lib.check(rc, "kf_linattn_fwd")
+        check(out, orc.linear_attention(qkv.cpu(), heads, dim), 1e-4)
+        ctrl = ws[:256].view(torch.int32).cpu()
+        assert not ctrl.any(), ctrl[:4]
+    bad = ctypes.c_void_p(ws.data_ptr() + 16)
+    rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), bad, big, 1, 64, H, dim, 1, 1e-15, _lib.KF_BF16,
+                            _lib.KF_F32, stream)
+    assert rc == 3 and b"aligned" in lib.kf_last_error()
+
+
+def test_graph_replay_and_streams():
+    """The fused launch inside a HIP graph: replays after eager calls and
+    between them give the eager bits each time (the counters return to zero
+    after every replay), also from a second stream with its own workspace."""
+    qkv = randn((2, 777, 3, 12 * 32), torch.bfloat16, seed=9).to(DEV)
+    run = qkv_attn_matmul(2, 12, 32, 777, dtype="bfloat16", output_dtype="float")
+    eager = run(qkv)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        on_side = run(qkv)
+    torch.cuda.current_stream().wait_stream(side)
+    assert torch.equal(on_side, eager)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run(qkv)
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        assert torch.equal(run(qkv), eager)

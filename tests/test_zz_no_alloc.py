@@ -28,7 +28,7 @@ def _run_both(B, N, H, D, in_dtype, out_dtype, seed):
     splits = int(lib.kf_linattn_default_splits(B, H, D, N))
     ws_bytes = int(lib.kf_linattn_workspace_bytes(B, H, D, splits))
     assert ws_bytes <= lib.kf_linattn_noalloc_max_bytes()
-    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    ws = torch.zeros(ws_bytes, device=DEV, dtype=torch.uint8)  # control words start at zero
     ref_out = torch.empty(B, N, H * D, device=DEV, dtype=out_dtype)
     out = torch.full((B, N, H * D), float("nan"), device=DEV, dtype=out_dtype)
     kin, kout = _lib.kf_dtype(in_dtype), _lib.kf_dtype(out_dtype)
