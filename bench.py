@@ -216,6 +216,49 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
                 roofline_frac=tflops / BF16_PEAK_TFLOPS)
 
 
+def bench_proj(kind: str, B: int, N: int, C: int, steps: int, warmup: int) -> dict:
+    """SANA projection GEMM (kf_proj_gemm, nn.Linear weight layout): "qkv" is
+    x[B*N, C] . W[3C, C]^T without bias, "out" is x . W[C, C]^T + bias.  The
+    same product through torch.matmul / torch.addmm (hipBLASLt) is timed
+    beside it as "library_us" (a reference point, not part of this build)."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    M, K = B * N, C
+    n_out = 3 * C if kind == "qkv" else C
+    g = _gen(11)
+    w = (torch.randn(n_out, K, generator=g) / K ** 0.5).to(torch.bfloat16).to("cuda")
+    bias = torch.randn(n_out, generator=g).to(torch.bfloat16).to("cuda") if kind == "out" else None
+    n_sets = _sets_for(M * K * 2 + M * n_out * 2)
+    xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to("cuda") for _ in range(n_sets)]
+    ys = [torch.empty(M, n_out, device="cuda", dtype=torch.bfloat16) for _ in range(n_sets)]
+    stream = _lib.stream_of(xs[0])
+    bp = _lib.ptr(bias)
+
+    def launch(i):
+        rc = lib.kf_proj_gemm(_lib.ptr(xs[i]), _lib.ptr(w), bp, _lib.ptr(ys[i]), M, n_out, K, K, n_out,
+                              _lib.KF_WEIGHT_NK, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_proj_gemm")
+
+    us, n_warm = _time_launches(launch, n_sets, steps, warmup)
+    wt = w.t()
+
+    def library(i):
+        if bias is None:
+            torch.matmul(xs[i], wt, out=ys[i])
+        else:
+            torch.addmm(bias, xs[i], wt, out=ys[i])
+
+    lib_us, _ = _time_launches(library, n_sets, steps, warmup)
+    flops = 2 * M * n_out * K
+    tflops = flops / (us * 1e-6) / 1e12
+    return dict(kernel="proj_gemm_kernel", workload=f"proj_{kind}_bf16_M{M}_N{n_out}_K{K}", us=us, flops=flops,
+                warmup_launches=n_warm, steps=steps, sets=n_sets, tflops=tflops,
+                roofline_frac=tflops / BF16_PEAK_TFLOPS, library_us=lib_us,
+                library_tflops=flops / (lib_us * 1e-6) / 1e12)
+
+
 def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
     """HBM stream ceiling: the library's 16-byte-per-lane copy kernel (kfm_copy,
     kernelforge_amd/csrc/measure.hip) reading and writing `nbytes` each, the
@@ -358,7 +401,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
-                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|copy2048|copy4096|copy8192|mfma), e.g. under rocprofv3")
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|copy2048|copy4096|copy8192|mfma), e.g. under rocprofv3")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="GPU time of untimed launches after the warm-up steps (clock settling)")
@@ -384,6 +427,8 @@ def main() -> int:
         "fa_jvp": lambda: bench_fa("jvp", max(10, steps // 5), max(3, warmup // 2)),
         "fa_fwd": lambda: bench_fa("fwd", max(10, steps // 5), max(3, warmup // 2)),
         "fa_bwd": lambda: bench_fa("bwd", max(10, steps // 5), max(3, warmup // 2)),
+        "proj_qkvA": lambda: bench_proj("qkv", 2, 4096, 2240, steps, warmup),
+        "proj_outA": lambda: bench_proj("out", 2, 4096, 2240, steps, warmup),
         "copy2048": lambda: bench_copy(16384 * 2048 * 2, steps, warmup),
         "copy4096": lambda: bench_copy(16384 * 4096 * 2, steps, warmup),
         "copy8192": lambda: bench_copy(16384 * 8192 * 2, steps, warmup),

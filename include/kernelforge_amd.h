@@ -232,6 +232,35 @@ int kf_rope_packed(void* qkv, const float* cos, const float* sin,
                    int dtype, kf_stream_t stream);
 
 /* ------------------------------------------------------------------ */
+/* SANA projections                                                    */
+/* ------------------------------------------------------------------ */
+
+#define KF_WEIGHT_NK 0 /* weight[n][k]: torch.nn.Linear.weight          */
+#define KF_WEIGHT_KN 1 /* weight_t[k][n]: the reference's prepacked WeightT */
+
+/*
+ * y[i, j] = dt( sum_c x[i, c] * W[j, c] (+ bias[j]) ), fp32 accumulation,
+ * the bias (when not NULL) added in fp32, one round-to-nearest-even to the
+ * storage dtype at the end.
+ *
+ * Replaces the TileLang kernels
+ *   _qkv_projection(batch, seq_len, channels, dtype)   SANA_LinearAttention/custom.py:23-85
+ *     (no bias, WeightT [C, 3C]), and
+ *   _output_projection(batch, seq_len, channels, dtype) SANA_LinearAttention/custom.py:457-523
+ *     (bias, WeightT [C, C]),
+ * with m = batch * seq_len rows.
+ *
+ * x: [m, ldx] (first k columns used); y: [m, ldy] (first n columns written);
+ * weight: dense [n, k] (KF_WEIGHT_NK) or [k, n] (KF_WEIGHT_KN); bias: [n] or
+ * NULL; all of `dtype` (KF_BF16 or KF_F16).  n % 8 == 0, k % 8 == 0,
+ * ldx % 8 == 0, ldy % 4 == 0; x and weight 16-byte aligned, y and bias 8-byte
+ * aligned.  m == 0 is a no-op.
+ */
+int kf_proj_gemm(const void* x, const void* weight, const void* bias, void* y,
+                 int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldy,
+                 int weight_layout, int dtype, kf_stream_t stream);
+
+/* ------------------------------------------------------------------ */
 /* FlashAttention forward and JVP                                      */
 /* ------------------------------------------------------------------ */
 

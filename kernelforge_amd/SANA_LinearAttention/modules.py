@@ -13,15 +13,16 @@ Mirrors the module API around the attention hot path:
 
 Data path of ``forward(x[B, N, C])``:
 
-1. ``qkv = x @ Wqkv^T (+ b)`` -- a plain library GEMM (hipBLASLt through
-   ``torch.nn.functional.linear``) into the packed ``[B, N, 3, C]`` layout.
+1. ``qkv = x @ Wqkv^T (+ b)`` -- the hand-written MFMA GEMM (``kf_proj_gemm``,
+   projection.py) on the module's ``[3C, C]`` weight, into the packed
+   ``[B, N, 3, C]`` layout.
 2. ``qk_norm``: RMSNorm over the C channels of each token's q and k, in place
    in the packed buffer (``kf_rmsnorm_fwd_strided``, no copies).
 3. ``rotary_emb = (cos, sin)``: rotary embedding of q and k, in place in the
    packed buffer (``kf_rope_packed``; original.py:136-138).
 4. ReLU linear attention (``kf_linattn_fwd``: split states on MFMA, fixed-order
    split reduction, MFMA output contraction), fp32 arithmetic.
-5. ``y = out @ Wproj^T + b`` -- library GEMM with the bias in its epilogue.
+5. ``y = out @ Wproj^T + b`` -- the same GEMM with the bias in its epilogue.
 
 Forward only: the linear-attention and rotary kernels have no backward, so
 ``forward`` raises ``RuntimeError`` when autograd would need one (grad mode on
@@ -49,6 +50,7 @@ from torch import nn
 from .. import _lib
 from ..rmsnorm.custom import RMSNorm, rms_norm_rows_
 from .custom import THREADS, linear_attention
+from .projection import TORCH_DTYPES, linear, qkv_projection  # noqa: F401  (re-exported)
 
 def apply_rotary_emb(x: torch.Tensor, freqs_cis, use_real: bool = True, use_real_unbind_dim: int = -1):
     """Rotary embedding with the reference's signature (SANA_LinearAttention/original.py:14-58).
@@ -82,53 +84,23 @@ def apply_rotary_emb(x: torch.Tensor, freqs_cis, use_real: bool = True, use_real
     return torch.stack((re, im), dim=stack_dim).flatten(*flat).to(x.dtype)
 
 
-# torch dtype -> reference dtype string (SANA_LinearAttention/custom.py:16-20).
-TORCH_DTYPES = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float"}
-
-
-class _QKVProjection:
-    """``kernel(X[B, N, C], WeightT[C, 3C]) -> QKV[B, N, 3C]`` for one shape."""
-
-    def __init__(self, batch: int, seq_len: int, channels: int, dtype: torch.dtype):
-        self.shape = (batch, seq_len, channels)
-        self.channels = channels
-        self.dtype = dtype
-
-    def __call__(self, X: torch.Tensor, WeightT: torch.Tensor) -> torch.Tensor:
-        if tuple(X.shape) != self.shape or X.dtype != self.dtype:
-            raise ValueError(f"X must be {self.dtype} of shape {self.shape}, got {X.dtype} {tuple(X.shape)}")
-        if tuple(WeightT.shape) != (self.channels, 3 * self.channels) or WeightT.dtype != self.dtype:
-            raise ValueError(f"WeightT must be {self.dtype} of shape ({self.channels}, {3 * self.channels})")
-        _lib.require_gpu(X, WeightT)
-        return torch.matmul(X, WeightT)
-
-
-def qkv_projection(batch: int, seq_len: int, channels: int, dtype: str = "bfloat16"):
-    """Return the no-bias QKV projection for one shape (SANA_LinearAttention/custom.py:83-85)."""
-    dtypes = {v: k for k, v in TORCH_DTYPES.items()}
-    if dtype not in dtypes:
-        raise ValueError(f"unsupported projection dtype: {dtype}")
-    return _QKVProjection(batch, seq_len, channels, dtypes[dtype])
-
-
 def _project_qkv(x: torch.Tensor, weight: torch.Tensor, bias, q_norm_weight, k_norm_weight,
                  norm_eps: float) -> torch.Tensor:
-    """``x[B, N, C] -> qkv[B, N, 3, C]``: library GEMM, then the optional q/k
-    RMSNorm over C in place in the packed buffer (original.py:122-130)."""
+    """``x[B, N, C] -> qkv[B, N, 3, C]``: the MFMA projection GEMM, then the
+    optional q/k RMSNorm over C in place in the packed buffer (original.py:122-130)."""
     B, N, C = x.shape
-    qkv = torch.nn.functional.linear(x, weight, bias).reshape(B, N, 3, C)
+    qkv = linear(x, weight.detach(), None if bias is None else bias.detach()).reshape(B, N, 3, C)
     if q_norm_weight is not None:
         rms_norm_rows_(qkv[:, :, 0], q_norm_weight.detach().to(qkv.dtype), norm_eps)
         rms_norm_rows_(qkv[:, :, 1], k_norm_weight.detach().to(qkv.dtype), norm_eps)
     return qkv
 
 
-def _project_out_joint(out: torch.Tensor, weight: torch.Tensor, bias) -> torch.Tensor:
-    """``out[B, N, C] @ W^T + b`` with the bias added in the GEMM (custom.py:469-523)."""
-    B, N, C = out.shape
-    if bias is None:
-        bias = torch.zeros(weight.shape[0], device=out.device, dtype=out.dtype)
-    return torch.addmm(bias.to(out.dtype), out.reshape(-1, C), weight.t()).reshape(B, N, weight.shape[0])
+def _project_out(out: torch.Tensor, weight: torch.Tensor, bias) -> torch.Tensor:
+    """``out[B, N, C] @ W^T + b`` with the bias added in fp32 in the GEMM's
+    epilogue before its one rounding (custom.py:469-523; original.py:143's
+    ``nn.Linear``)."""
+    return linear(out, weight.detach(), None if bias is None else bias.detach())
 
 
 @torch.library.custom_op("kernelforge_amd::joint_litela_forward", mutates_args=(), device_types="cuda")
@@ -139,7 +111,7 @@ def _joint_litela_op(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Option
     """JointLiteLA's forward as one opaque operator (SANA_LinearAttention/custom.py:885-898)."""
     _lib.require_gpu(x)
     qkv = _project_qkv(x, qkv_weight, qkv_bias, q_norm_weight, k_norm_weight, norm_eps)
-    return _project_out_joint(linear_attention(qkv, heads, dim, eps, x.dtype), proj_weight, proj_bias)
+    return _project_out(linear_attention(qkv, heads, dim, eps, x.dtype), proj_weight, proj_bias)
 
 
 @_joint_litela_op.register_fake
@@ -230,7 +202,7 @@ class LiteLA(nn.Module):
         _lib.require_gpu(x)
         _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return self.proj(out)
+        return _project_out(out, self.proj.weight, self.proj.bias)
 
 
 class CustomLiteLA(LiteLA):
@@ -260,7 +232,7 @@ class CustomLiteLA(LiteLA):
         _lib.require_gpu(x)
         _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return self.proj(out)
+        return _project_out(out, self.proj.weight, self.proj.bias)
 
 
 class JointLiteLA(CustomLiteLA):
@@ -281,7 +253,7 @@ class JointLiteLA(CustomLiteLA):
         _lib.require_gpu(x)
         _require_inference(self, x)
         out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return _project_out_joint(out, self.proj.weight, self.proj.bias)
+        return _project_out(out, self.proj.weight, self.proj.bias)
 
 
 class CustomOpJointLiteLA(JointLiteLA):

@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libkernelforge_amd.so"
 ABI_VERSION = 1
 
 KF_F32, KF_F16, KF_BF16 = 0, 1, 2
+KF_WEIGHT_NK, KF_WEIGHT_KN = 0, 1
 TORCH_TO_KF = {torch.float32: KF_F32, torch.float16: KF_F16, torch.bfloat16: KF_BF16}
 
 _c_void_p = ctypes.c_void_p
@@ -52,6 +53,8 @@ SIGNATURES = {
     "kf_linattn_noalloc_max_bytes": (_i64, []),
     "kf_linattn_fwd_noalloc": (
         _int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p]),
+    "kf_proj_gemm": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p]),
     "kf_rope_packed": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "kf_fa_fwd": (
         _int,

@@ -1,0 +1,159 @@
+"""GPU parity of the SANA projection GEMM (kf_proj_gemm; the reference's
+_qkv_projection and _output_projection, SANA_LinearAttention/custom.py:23-85 and
+:457-523).
+
+The reference computes ``Cast(dtype, sum_k x*W (fp32 fragment) + float(bias))``.
+Two checks pin that without trusting any GPU library:
+
+- integer-valued inputs, small enough that every fp32 partial sum is exact in
+  any order: the result must equal the fp64 product rounded once to the
+  dtype, bit for bit (a wrong index, a dropped or doubled K chunk, a stale LDS
+  stage or a second rounding all change bits);
+- random inputs: |y - y64| <= K 2^-24 sum_k |x||w| (worst-case fp32
+  accumulation in any order) + half an ulp of the dtype (the one rounding),
+  against the fp64 product.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from kernelforge_amd import _lib
+from kernelforge_amd.SANA_LinearAttention.projection import (linear, linear_t, output_projection,
+                                                              qkv_projection)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+UNIT_ROUNDOFF = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24}
+
+
+def _ints(shape, lo, hi, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(lo, hi + 1, shape, generator=g).to(dtype)
+
+
+def _ref64(x, w, b=None):
+    y = x.double() @ w.double().T
+    return y if b is None else y + b.double()
+
+
+def _bound(x, w, y64, dtype):
+    k = x.shape[-1]
+    acc = k * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T)
+    return acc + UNIT_ROUNDOFF[dtype] * y64.abs() + 2.0 ** -24 * (y64.abs() + 1e-30) + 6e-8
+
+
+SHAPES = [  # (M, N, K): full tiles, ragged rows/columns, a K tail of one chunk, tiny
+    (512, 512, 256),
+    (300, 264, 1160),
+    (1, 8, 8),
+    (777, 1152, 1152),
+    (96, 288, 96),
+]
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("layout", ("nk", "kn"))
+@pytest.mark.parametrize("bias", (False, True))
+def test_integer_inputs_round_once_bit_exact(dtype, layout, bias):
+    for i, (M, N, K) in enumerate(SHAPES):
+        print(f"proj int case dtype={dtype} layout={layout} bias={bias} M={M} N={N} K={K}", flush=True)
+        x = _ints((M, K), -3, 3, 10 + i, dtype)
+        w = _ints((N, K), -3, 3, 20 + i, dtype)
+        b = _ints((N,), -50, 50, 30 + i, dtype) if bias else None
+        xd, bd = x.to(DEV), (b.to(DEV) if bias else None)
+        if layout == "nk":
+            y = linear(xd, w.to(DEV), bd)
+        else:
+            y = linear_t(xd, w.T.contiguous().to(DEV), bd)
+        torch.cuda.synchronize()
+        expect = _ref64(x, w, b).to(dtype)
+        assert torch.equal(y.cpu(), expect), (M, N, K)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+def test_random_inputs_within_the_accumulation_bound(dtype):
+    for M, N, K in ((1024, 6720, 2240), (333, 2240, 2240), (64, 3456, 1152)):
+        print(f"proj random case dtype={dtype} M={M} N={N} K={K}", flush=True)
+        g = torch.Generator().manual_seed(M + N + K)
+        x = torch.randn(M, K, generator=g).to(dtype)
+        w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dtype)
+        b = torch.randn(N, generator=g).to(dtype)
+        y = linear(x.to(DEV), w.to(DEV), b.to(DEV)).cpu().double()
+        y64 = _ref64(x, w, b)
+        err = (y - y64).abs()
+        bound = _bound(x, w, y64, dtype)
+        assert bool((err <= bound).all()), float((err - bound).max())
+        # The bound is tight enough to see one dropped 8-element K chunk.
+        dropped = _ref64(x[:, 8:], w[:, 8:], b)
+        assert bool(((dropped - y64).abs() > bound).any())
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+def test_weight_layouts_agree_bitwise(dtype):
+    """The [N, K] and the prepacked [K, N] weight feed the same operands to the
+    same MFMA sequence: identical bits."""
+    g = torch.Generator().manual_seed(5)
+    M, N, K = 700, 1400, 1160
+    x = torch.randn(M, K, generator=g).to(dtype).to(DEV)
+    w = torch.randn(N, K, generator=g).to(dtype).to(DEV)
+    b = torch.randn(N, generator=g).to(dtype).to(DEV)
+    assert torch.equal(linear(x, w, b), linear_t(x, w.T.contiguous(), b))
+
+
+def test_strided_rows_and_untouched_padding():
+    """ldx > K with NaN padding beyond K (never read) and ldy > N (padding
+    columns never written), through the C ABI."""
+    lib = _lib.load()
+    M, N, K, ldx, ldy = 300, 264, 520, 520 + 24, 264 + 12
+    x = _ints((M, ldx), -3, 3, 1, torch.bfloat16)
+    x[:, K:] = float("nan")
+    w = _ints((N, K), -3, 3, 2, torch.bfloat16)
+    xd, wd = x.to(DEV), w.to(DEV)
+    y = torch.full((M, ldy), 7.0, dtype=torch.bfloat16, device=DEV)
+    rc = lib.kf_proj_gemm(_lib.ptr(xd), _lib.ptr(wd), None, _lib.ptr(y), M, N, K, ldx, ldy, _lib.KF_WEIGHT_NK,
+                          _lib.KF_BF16, _lib.stream_of(xd))
+    _lib.check(rc, "kf_proj_gemm")
+    y = y.cpu()
+    assert torch.equal(y[:, :N], _ref64(x[:, :K], w).to(torch.bfloat16))
+    assert bool((y[:, N:] == 7.0).all())
+
+
+def test_strided_input_view():
+    """linear() on a column slice of a wider buffer uses its row stride."""
+    g = torch.Generator().manual_seed(9)
+    big = torch.randn(2, 130, 3 * 256, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(512, 256, generator=g) / 16).to(torch.bfloat16).to(DEV)
+    view = big[:, :, 256:512]
+    assert torch.equal(linear(view, w), linear(view.contiguous(), w))
+
+
+def test_reference_factories():
+    """qkv_projection / output_projection keep the reference's call signatures
+    (WeightT layouts, shape and dtype checks) and match linear()."""
+    B, N, C = 2, 200, 256
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16).to(DEV)
+    w_qkv = (torch.randn(3 * C, C, generator=g) / 16).to(torch.bfloat16).to(DEV)
+    w_out = (torch.randn(C, C, generator=g) / 16).to(torch.bfloat16).to(DEV)
+    b_out = torch.randn(C, generator=g).to(torch.bfloat16).to(DEV)
+    qkv = qkv_projection(B, N, C, "bfloat16")(x, w_qkv.t().contiguous())
+    assert qkv.shape == (B, N, 3 * C) and torch.equal(qkv, linear(x, w_qkv))
+    y = output_projection(B, N, C, "bfloat16")(x, w_out.t().contiguous(), b_out)
+    assert torch.equal(y, linear(x, w_out, b_out))
+    with pytest.raises(ValueError, match="WeightT"):
+        qkv_projection(B, N, C, "bfloat16")(x, w_qkv)
+    with pytest.raises(ValueError, match="X must be"):
+        output_projection(B, N, C, "bfloat16")(x[:, 1:], w_out, b_out)
+
+
+def test_host_rejections():
+    lib = _lib.load()
+    null = ctypes.c_void_p(0)
+    assert lib.kf_proj_gemm(null, null, null, null, 4, 12, 16, 16, 12, 0, _lib.KF_BF16, null) == 1
+    assert b"multiples of 8" in lib.kf_last_error()
+    assert lib.kf_proj_gemm(null, null, null, null, 0, 16, 16, 16, 16, 0, _lib.KF_BF16, null) == 0
+    with pytest.raises(ValueError, match="multiples of 8"):
+        linear(torch.zeros(3, 12, device=DEV, dtype=torch.bfloat16), torch.zeros(16, 12, device=DEV,
+                                                                                    dtype=torch.bfloat16))
