@@ -31,7 +31,6 @@
 namespace kf {
 namespace {
 
-constexpr int kGemmThreads = 512;  // 8 wavefronts
 constexpr int kGroupM = 8;         // tile rows walked before the next tile column
 
 struct GemmParams {
@@ -44,18 +43,33 @@ struct GemmParams {
     int tiles_m, tiles_n;
 };
 
-template <typename T, int BM_, int BN_, int WAVES_M_, int STAGES_, bool KN_> struct GemmCfg {
+template <typename T, int BM_, int BN_, int WAVES_M_, int STAGES_, bool KN_, int ROWB_ = 128, int WAVES_ = 8>
+struct GemmCfg {
+    typedef T Elem;
     static constexpr int BM = BM_, BN = BN_, STAGES = STAGES_;
+    static constexpr int WAVES = WAVES_, THREADS = 64 * WAVES;
     static constexpr bool KN = KN_;
+    static constexpr int ROWB = ROWB_;                // bytes of K per tile row and stage: 64 or 128
     static constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-    static constexpr int BK = 8 * EPC;               // K elements per stage: 128-byte rows
-    static constexpr int WAVES_M = WAVES_M_, WAVES_N = 8 / WAVES_M_;
+    static constexpr int CPR = ROWB / 16;             // chunks per tile row
+    static constexpr int BK = ROWB / (int)sizeof(T);  // K elements per stage
+    static constexpr int STEPS = ROWB / 64;           // MFMA K steps per stage (64 bytes each)
+    static constexpr int RPC = 64 / CPR;              // tile rows per copy instruction
+    static constexpr int WAVES_M = WAVES_M_, WAVES_N = WAVES / WAVES_M_;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int MB = WM / 16, NB = WN / 16;
     static constexpr int XS = BM * BK, WS = BN * BK;  // elements per stage
-    static constexpr int XI = BM / 64, WI = BN / 64;  // copies per wavefront per stage
+    // Copies per wavefront per stage (the fewest any wavefront issues when a
+    // tile side is not a whole number of copy rounds).
+    static constexpr int XI = BM / (WAVES * RPC), WI = BN / (WAVES * RPC);
+    // Workgroups per CU the kernel is shaped for (LDS allows two when a
+    // workgroup takes at most half of it).
+    static constexpr int OCC = WAVES == 4 ? 2 : 1;
     static constexpr int LDS_BYTES = STAGES * (XS + WS) * (int)sizeof(T);
-    static_assert(BM % 64 == 0 && BN % 64 == 0, "tiles are whole copy rounds");
+    static_assert(ROWB == 64 || ROWB == 128, "row geometry");
+    static_assert(BM % (WAVES * RPC) == 0 && BN % 16 == 0, "activation tiles are whole copy rounds; 16-row blocks");
+    static_assert(WAVES == 8 || WAVES == 4, "workgroup shape");
+    static_assert(!KN || BN % 64 == 0, "WeightT tiles are whole copy rounds");
     static_assert(WM % 16 == 0 && WN % 16 == 0, "16x16 MFMA blocks");
     static_assert(!KN || BN == 128 || BN == 256, "the WeightT swizzles need 16..64 chunks per row");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS");
@@ -79,12 +93,16 @@ __device__ __forceinline__ void gemm_tile(int blk, int tiles_m, int tiles_n, int
     tn = r / gm;
 }
 
-// K-contiguous tile [R][BK] (128-byte rows): logical 16-byte chunk c of row r
-// sits at physical chunk c ^ kswz(r).  An operand read touches 16 consecutive
-// rows at one logical chunk; two rows share a 256-byte bank line, and the map
-// sends the 8 even and the 8 odd rows to 8 distinct chunks each, so the 16
-// lanes of a ds_read_b128 cycle hit 16 distinct 16-byte bank groups.
-__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
+// K-contiguous tile [R][BK] (rows of CPR 16-byte chunks): logical chunk c of
+// row r sits at physical chunk c ^ kswz(r).  An operand read touches 16
+// consecutive rows at one logical chunk; 256/(16 CPR) rows share a 256-byte
+// bank line, and the map sends the rows of each residue class to distinct
+// chunks, so the 16 lanes of a ds_read_b128 cycle hit 16 distinct 16-byte bank
+// groups.
+template <int CPR> __device__ __forceinline__ int kswz(int r) {
+    if constexpr (CPR == 8) return (r >> 1) & 7;
+    else return (r >> 2) & 3;
+}
 
 // WeightT tile [BK][BN]: logical chunk c of row k sits at c ^ nswz(k).
 // 16-bit: a transposing operand read of a 32-lane half touches rows
@@ -100,20 +118,22 @@ template <typename T> __device__ __forceinline__ int nswz(int k) {
 // Copy rows row0..row0+R-1 (clamped to rows_valid - 1: those rows only feed
 // outputs that are never stored), K columns k0..k0+BK-1 (zero past K) of a
 // K-contiguous matrix into a [R][BK] tile.  Instruction i covers tile rows
-// 8i..8i+7; wavefront w issues i = w, w + 8, ...
+// RPC i .. RPC i + RPC-1; wavefront w issues i = w, w + 8, ...
 template <typename T, typename C, int R>
 __device__ __forceinline__ void copy_krows(T* tile, const T* g, int64_t ld, int row0, int rows_valid, int k0,
                                            int K, int wave, int lane) {
+    constexpr int NI = R / C::RPC;
 #pragma unroll
-    for (int j = 0; j < R / 64; ++j) {
-        const int i = wave + 8 * j;
-        const int r = 8 * i + (lane >> 3);
-        const int c = (lane & 7) ^ kswz(r);
+    for (int j = 0; j < (NI + C::WAVES - 1) / C::WAVES; ++j) {
+        const int i = wave + C::WAVES * j;
+        if (NI % C::WAVES != 0 && i >= NI) break;
+        const int r = C::RPC * i + lane / C::CPR;
+        const int c = (lane % C::CPR) ^ kswz<C::CPR>(r);
         const int gr = min(row0 + r, rows_valid - 1);
         const int kk = k0 + C::EPC * c;
         const void* src = kk < K ? static_cast<const void*>(g + (int64_t)gr * ld + kk)
                                  : static_cast<const void*>(g_zero16);
-        lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + 8 * i * C::BK)));
+        lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + C::RPC * i * C::BK)));
     }
 }
 
@@ -122,10 +142,10 @@ __device__ __forceinline__ void copy_krows(T* tile, const T* g, int64_t ld, int 
 template <typename T, typename C>
 __device__ __forceinline__ void copy_kn(T* tile, const T* g, int N, int n0, int k0, int K, int wave, int lane) {
     constexpr int CH = C::BN / C::EPC, RPI = 64 / CH, NI = C::BK / RPI;
-    static_assert(NI == 8 * C::WI, "copy rounds");
+    static_assert(NI == C::WAVES * C::WI, "copy rounds");
 #pragma unroll
-    for (int j = 0; j < NI / 8; ++j) {
-        const int i = wave + 8 * j;
+    for (int j = 0; j < NI / C::WAVES; ++j) {
+        const int i = wave + C::WAVES * j;
         const int r = RPI * i + lane / CH;
         const int c = (lane % CH) ^ nswz<T>(r);
         const int kk = k0 + r, nn = n0 + C::EPC * c;
@@ -140,7 +160,7 @@ __device__ __forceinline__ void copy_kn(T* tile, const T* g, int N, int n0, int 
 template <typename T, typename C>
 __device__ __forceinline__ u32x4 op_krows(const T* tile, int r0, int s, int lane) {
     const int r = r0 + (lane & 15);
-    const int c = (4 * s + (lane >> 4)) ^ kswz(r);
+    const int c = (4 * s + (lane >> 4)) ^ kswz<C::CPR>(r);
     return *reinterpret_cast<const u32x4*>(tile + r * C::BK + c * C::EPC);
 }
 
@@ -199,15 +219,19 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Wait until the copies of stage kt have landed when `ahead` later stages
-// (0 .. STAGES-2) have been issued behind it.
-template <int STAGES, int PER> __device__ __forceinline__ void wait_stage(int ahead) {
-    if constexpr (STAGES >= 4) {
-        if (ahead >= 2) { wait_vmcnt<2 * PER>(); return; }
+// (0 .. STAGES-2) have been issued behind it.  Loads retire in order, so
+// allowing PER * ahead outstanding (PER = the fewest copies any wavefront
+// issues per stage) is sufficient for every wavefront.
+template <int STAGES, int PER, int A = STAGES - 2> __device__ __forceinline__ void wait_stage(int ahead) {
+    if constexpr (A > 0) {
+        if (ahead >= A) {
+            wait_vmcnt<A * PER>();
+            return;
+        }
+        wait_stage<STAGES, PER, A - 1>(ahead);
+    } else {
+        wait_vmcnt<0>();
     }
-    if constexpr (STAGES >= 3) {
-        if (ahead >= 1) { wait_vmcnt<PER>(); return; }
-    }
-    wait_vmcnt<0>();
 }
 
 // Accumulate one wavefront's WM x WN sub-tile over the whole K range.
@@ -245,7 +269,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, T* lds, int m
         const T* xs = lds + (kt % C::STAGES) * (C::XS + C::WS);
         const T* ws = xs + C::XS;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < C::STEPS; ++s) {
             u32x4 a[C::NB], b[C::MB];
 #pragma unroll
             for (int nb = 0; nb < C::NB; ++nb) {
@@ -275,7 +299,7 @@ template <typename T> __device__ __forceinline__ void store4(T* dst, f32x4 v, co
 }
 
 template <typename T, typename C, bool BIAS>
-__global__ __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void proj_gemm_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(16))) T lds[C::STAGES * (C::XS + C::WS)];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -306,19 +330,61 @@ void proj_gemm_kernel(GemmParams p) {
     }
 }
 
-// Tile shape: 256 x 256, 2 x 4 wavefronts of 128 x 64 (128 accumulator
-// registers per lane, two wavefronts per SIMD), two 64 KiB LDS stages.
-template <typename T, bool KN> using ProjCfg = GemmCfg<T, 256, 256, 2, 2, KN>;
+// Tile shapes: 256 activation rows times BN output channels, 8 wavefronts of
+// 64 x BN/2 (4 x 2; 4 x 2 measured faster than 2 x 4 at BN = 256), two
+// 128-byte-row LDS stages (three for BN = 128).  The WeightT layout's swizzle
+// needs BN = 128 or 256.
+template <typename T, int BN, bool KN> struct ProjTile {
+    typedef GemmCfg<T, 256, BN, 4, BN == 128 ? 3 : 2, KN> C;
+};
 
-template <typename T, bool KN>
-int launch_gemm(GemmParams p, bool bias, hipStream_t stream) {
-    typedef ProjCfg<T, KN> C;
+template <typename C>
+int launch_cfg(GemmParams p, bool bias, hipStream_t stream) {
     p.tiles_m = (p.M + C::BM - 1) / C::BM;
     p.tiles_n = (p.N + C::BN - 1) / C::BN;
     const int grid = p.tiles_m * p.tiles_n;
-    if (bias) hipLaunchKernelGGL((proj_gemm_kernel<T, C, true>), dim3(grid), dim3(kGemmThreads), 0, stream, p);
-    else hipLaunchKernelGGL((proj_gemm_kernel<T, C, false>), dim3(grid), dim3(kGemmThreads), 0, stream, p);
+    if (bias) hipLaunchKernelGGL((proj_gemm_kernel<typename C::Elem, C, true>), dim3(grid), dim3(C::THREADS), 0, stream, p);
+    else hipLaunchKernelGGL((proj_gemm_kernel<typename C::Elem, C, false>), dim3(grid), dim3(C::THREADS), 0, stream, p);
     return check_launch("proj_gemm_kernel");
+}
+
+// Output-tile width for an M x N problem.  One workgroup runs per CU, so the
+// launch takes ceil(tiles / CUs) rounds, and a round costs about BN + 32
+// (work proportional to the width plus a fixed per-tile part; this model ranks
+// the measured times of every candidate correctly at the SANA shapes).
+inline int pick_bn(int M, int N, const int* cands, int n_cands) {
+    const int cus = device_cu_count();
+    int best = cands[0];
+    long long best_cost = -1;
+    for (int i = 0; i < n_cands; ++i) {
+        const int bn = cands[i];
+        const long long tiles = (long long)((M + 255) / 256) * ((N + bn - 1) / bn);
+        const long long cost = (tiles + cus - 1) / cus * (bn + 32);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = bn;
+        }
+    }
+    return best;
+}
+
+template <typename T, bool KN>
+int launch_gemm(const GemmParams& p, bool bias, hipStream_t st) {
+    // 16-bit weights in [N][K]: five widths; fp32 or WeightT: 256 and 128.
+    if constexpr (sizeof(T) == 2 && !KN) {
+        static const int cands[] = {224, 256, 192, 160, 128};
+        switch (pick_bn(p.M, p.N, cands, 5)) {
+        case 256: return launch_cfg<typename ProjTile<T, 256, KN>::C>(p, bias, st);
+        case 224: return launch_cfg<typename ProjTile<T, 224, KN>::C>(p, bias, st);
+        case 192: return launch_cfg<typename ProjTile<T, 192, KN>::C>(p, bias, st);
+        case 160: return launch_cfg<typename ProjTile<T, 160, KN>::C>(p, bias, st);
+        default: return launch_cfg<typename ProjTile<T, 128, KN>::C>(p, bias, st);
+        }
+    } else {
+        static const int cands[] = {256, 128};
+        if (pick_bn(p.M, p.N, cands, 2) == 256) return launch_cfg<typename ProjTile<T, 256, KN>::C>(p, bias, st);
+        return launch_cfg<typename ProjTile<T, 128, KN>::C>(p, bias, st);
+    }
 }
 
 template <typename T> int launch_gemm_layout(const GemmParams& p, int layout, bool bias, hipStream_t st) {

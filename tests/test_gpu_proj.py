@@ -72,6 +72,22 @@ def test_integer_inputs_round_once_bit_exact(dtype, layout, bias):
         assert torch.equal(y.cpu(), expect), (M, N, K)
 
 
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_every_tile_width(dtype):
+    """The launch picks the output-tile width (256, 224, 192, 160 or 128
+    channels) from the shape; on a 256-CU MI355X these shapes select each of
+    them (16384x2048 -> 256, 8192x6720 -> 224, 8192x1536 -> 192,
+    8192x2240 -> 160, 300x264 -> 128).  K = 72 adds a one-chunk K tail."""
+    K = 72
+    for i, (M, N) in enumerate(((16384, 2048), (8192, 6720), (8192, 1536), (8192, 2240), (300, 264))):
+        print(f"proj width case dtype={dtype} M={M} N={N} K={K}", flush=True)
+        x = _ints((M, K), -3, 3, 40 + i, dtype)
+        w = _ints((N, K), -3, 3, 50 + i, dtype)
+        b = _ints((N,), -50, 50, 60 + i, dtype)
+        y = linear(x.to(DEV), w.to(DEV), b.to(DEV)).cpu()
+        assert torch.equal(y, _ref64(x, w, b).to(dtype)), (M, N)
+
+
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
 def test_random_inputs_within_the_accumulation_bound(dtype):
     for M, N, K in ((1024, 6720, 2240), (333, 2240, 2240), (64, 3456, 1152)):
