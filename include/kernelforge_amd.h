@@ -260,6 +260,36 @@ int kf_proj_gemm(const void* x, const void* weight, const void* bias, void* y,
                  int64_t m, int64_t n, int64_t k, int64_t ldx, int64_t ldy,
                  int weight_layout, int dtype, kf_stream_t stream);
 
+/*
+ * LiteLA attention with the QKV projection fused in, up to (not including)
+ * the output projection, head dim 32:
+ *   q, k, v = dt(x W^T + bias)       (W = qkv_weight [3C, C], rows q | k | v)
+ *   out[b, t, 32h + r] = dt( sum_c S[r][c] relu(q[t][32h+c])
+ *                            / (sum_c z[c] relu(q[t][32h+c]) + eps) ),
+ *   S[r][c] = sum_t v[t][32h+r] relu(k[t][32h+c]),  z[c] = sum_t relu(k[t][32h+c])
+ * with q, k, v never written to memory.  C = 32 * heads.
+ *
+ * Replaces the fused projection kernels of GroupedFull64QOutLiteLA
+ *   grouped_full64_kv_vk_producer / partial_reduce_joint_qout
+ *     SANA_LinearAttention/custom.py:606-809
+ * (there for B=1, N=1024, C=1152 only) for any batch, length and head count.
+ *
+ * x, out: [batch, seq_len, C]; qkv_weight: [3C, C]; qkv_bias: [3C] or NULL;
+ * all of `dtype` (KF_BF16 or KF_F16); x, qkv_weight and out 16-byte aligned.
+ * dim must be 32 (KF_E_UNSUPPORTED otherwise).  Three launches: k/v
+ * projection with the per-(batch, head, 256-token tile) state partials, their
+ * fixed-order sum (deterministic), q projection with the output.  The
+ * workspace holds the partials and states: at least
+ * kf_litela_fused_workspace_bytes(batch, seq_len, heads) bytes, 256-byte
+ * aligned, no initialisation needed.  Calls that share a workspace must not
+ * overlap.
+ */
+int64_t kf_litela_fused_workspace_bytes(int64_t batch, int64_t seq_len, int64_t heads);
+int kf_litela_fused_attn(const void* x, const void* qkv_weight, const void* qkv_bias, void* out,
+                         void* workspace, int64_t workspace_bytes,
+                         int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
+                         float eps, int dtype, kf_stream_t stream);
+
 /* ------------------------------------------------------------------ */
 /* FlashAttention forward and JVP                                      */
 /* ------------------------------------------------------------------ */

@@ -11,7 +11,18 @@ Mirrors the module API around the attention hot path:
 - ``qkv_projection`` -- the no-bias projection factory taking a prepacked
   ``WeightT[C, 3C]`` (SANA_LinearAttention/custom.py:83-85).
 
-Data path of ``forward(x[B, N, C])``:
+Data path of ``forward(x[B, N, C])`` -- fused (fused.py), when head dim is
+32, the dtype is 16-bit, there is no q/k norm or rotary embedding and the
+shape has enough work (``LiteLA.fused_projection`` = None chooses, True/False
+forces):
+
+1. ``kf_litela_fused_attn``: q, k and v projected tile by tile and consumed
+   in place (k/v -> ReLU -> state partials; fixed-order partial sum; q ->
+   output), never written to memory;
+2. ``y = out @ Wproj^T + b`` -- the projection GEMM with the bias in its
+   epilogue.
+
+Otherwise (unfused):
 
 1. ``qkv = x @ Wqkv^T (+ b)`` -- the hand-written MFMA GEMM (``kf_proj_gemm``,
    projection.py) on the module's ``[3C, C]`` weight, into the packed
@@ -50,6 +61,7 @@ from torch import nn
 from .. import _lib
 from ..rmsnorm.custom import RMSNorm, rms_norm_rows_
 from .custom import THREADS, linear_attention
+from .fused import fused_applicable, litela_fused_attention, prefer_fused
 from .projection import TORCH_DTYPES, linear, qkv_projection  # noqa: F401  (re-exported)
 
 def apply_rotary_emb(x: torch.Tensor, freqs_cis, use_real: bool = True, use_real_unbind_dim: int = -1):
@@ -96,6 +108,28 @@ def _project_qkv(x: torch.Tensor, weight: torch.Tensor, bias, q_norm_weight, k_n
     return qkv
 
 
+def _attention_output(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias, q_norm_weight, k_norm_weight,
+                      norm_eps: float, heads: int, dim: int, eps: float, fused: Optional[bool],
+                      rotary_fn=None) -> torch.Tensor:
+    """LiteLA's attention output before the output projection.  Without q/k
+    norm and rotary embedding, with head dim 32 and a 16-bit dtype, the fused
+    projection + attention kernels (fused.py) run when ``fused`` is True, or
+    when it is None and they pay for the shape; otherwise the projection GEMM
+    fills the packed qkv, the optional norm and rotation run in place, and the
+    linear-attention kernel follows."""
+    B, N, _ = x.shape
+    if q_norm_weight is None and rotary_fn is None and fused_applicable(x.dtype, dim):
+        if fused if fused is not None else prefer_fused(B, N, heads, x.device):
+            return litela_fused_attention(x, qkv_weight.detach(),
+                                          None if qkv_bias is None else qkv_bias.detach(), heads, eps)
+    qkv = _project_qkv(x, qkv_weight, qkv_bias, q_norm_weight, k_norm_weight, norm_eps)
+    if rotary_fn is not None:
+        rotary_fn(qkv)
+    # The kernel rounds its fp32 result straight to x's dtype (round to
+    # nearest even), as `.to(dtype)` on the fp32 result would.
+    return linear_attention(qkv, heads, dim, eps, x.dtype)
+
+
 def _project_out(out: torch.Tensor, weight: torch.Tensor, bias) -> torch.Tensor:
     """``out[B, N, C] @ W^T + b`` with the bias added in fp32 in the GEMM's
     epilogue before its one rounding (custom.py:469-523; original.py:143's
@@ -110,8 +144,8 @@ def _joint_litela_op(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Option
                      heads: int, dim: int, eps: float, norm_eps: float) -> torch.Tensor:
     """JointLiteLA's forward as one opaque operator (SANA_LinearAttention/custom.py:885-898)."""
     _lib.require_gpu(x)
-    qkv = _project_qkv(x, qkv_weight, qkv_bias, q_norm_weight, k_norm_weight, norm_eps)
-    return _project_out(linear_attention(qkv, heads, dim, eps, x.dtype), proj_weight, proj_bias)
+    out = _attention_output(x, qkv_weight, qkv_bias, q_norm_weight, k_norm_weight, norm_eps, heads, dim, eps, None)
+    return _project_out(out, proj_weight, proj_bias)
 
 
 @_joint_litela_op.register_fake
@@ -139,6 +173,8 @@ class LiteLA(nn.Module):
     """
 
     PAD_VAL = 1
+    # Fused projection + attention: None = chosen per shape, True / False = forced.
+    fused_projection: Optional[bool] = None
 
     def __init__(self, in_dim: int, out_dim: int, heads: int | None = None, heads_ratio: float = 1.0,
                  dim: int = 32, eps: float = 1e-15, use_bias: bool = False, qk_norm: bool = False,
@@ -171,12 +207,11 @@ class LiteLA(nn.Module):
             return None, None, 1e-5
         return self.q_norm.weight, self.k_norm.weight, self.q_norm.eps
 
-    def _packed_qkv(self, x: torch.Tensor, rotary_emb=None) -> torch.Tensor:
+    def _attn_out(self, x: torch.Tensor, rotary_emb=None) -> torch.Tensor:
         qn, kn, norm_eps = self._norm_weights()
-        qkv = _project_qkv(x, self.qkv.weight, self.qkv.bias, qn, kn, norm_eps)
-        if rotary_emb is not None:
-            self._rotate_(qkv, rotary_emb)
-        return qkv
+        rot = None if rotary_emb is None else (lambda qkv: self._rotate_(qkv, rotary_emb))
+        return _attention_output(x, self.qkv.weight, self.qkv.bias, qn, kn, norm_eps, self.heads, self.dim,
+                                 self.eps, self.fused_projection, rot)
 
     def _rotate_(self, qkv: torch.Tensor, rotary_emb) -> None:
         """q and k of the packed qkv rotated in place (original.py:136-138)."""
@@ -190,19 +225,13 @@ class LiteLA(nn.Module):
                                         _lib.kf_dtype(qkv.dtype), _lib.stream_of(qkv))
         _lib.check(rc, "kf_rope_packed")
 
-    def _attention(self, qkv: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-        # The kernel rounds its fp32 result straight to `dtype` (round to
-        # nearest even), as `.to(dtype)` on the fp32 result would.
-        return linear_attention(qkv, self.heads, self.dim, self.eps, dtype)
-
     def forward(self, x: torch.Tensor, mask=None, HW=None, rotary_emb=None, block_id=None,
                 block_mask=None) -> torch.Tensor:
         if x.dim() != 3 or x.shape[-1] != self.in_dim:
             raise ValueError(f"x must be [B, N, {self.in_dim}], got {tuple(x.shape)}")
         _lib.require_gpu(x)
         _require_inference(self, x)
-        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return _project_out(out, self.proj.weight, self.proj.bias)
+        return _project_out(self._attn_out(x, rotary_emb), self.proj.weight, self.proj.bias)
 
 
 class CustomLiteLA(LiteLA):
@@ -231,8 +260,7 @@ class CustomLiteLA(LiteLA):
         self._validate_input(x)
         _lib.require_gpu(x)
         _require_inference(self, x)
-        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return _project_out(out, self.proj.weight, self.proj.bias)
+        return _project_out(self._attn_out(x, rotary_emb), self.proj.weight, self.proj.bias)
 
 
 class JointLiteLA(CustomLiteLA):
@@ -252,8 +280,7 @@ class JointLiteLA(CustomLiteLA):
         self._validate_input(x)
         _lib.require_gpu(x)
         _require_inference(self, x)
-        out = self._attention(self._packed_qkv(x, rotary_emb), x.dtype)
-        return _project_out(out, self.proj.weight, self.proj.bias)
+        return _project_out(self._attn_out(x, rotary_emb), self.proj.weight, self.proj.bias)
 
 
 class CustomOpJointLiteLA(JointLiteLA):
@@ -309,10 +336,12 @@ GROUPED_HEADS, GROUPED_DIM = 36, 32
 class GroupedFull64QOutLiteLA(JointLiteLA):
     """The reference's shape-specialised LiteLA (SANA_LinearAttention/custom.py:812-861),
     with its constructor checks: exactly B=1, N=1024, C=1152, H=36, D=32, bf16,
-    ``qk_norm=False``, ``use_bias=False``, and no ``rotary_emb``.  The reference
-    fuses the QKV projection into its attention kernels for this one shape;
-    here it runs JointLiteLA's pipeline, whose attention kernels already
-    stream the packed qkv once."""
+    ``qk_norm=False``, ``use_bias=False``, and no ``rotary_emb``.  Like the
+    reference, it always runs the fused projection kernels (the k/v projection
+    with ReLU and the state partials, then the q projection with the output;
+    kf_litela_fused_attn), followed by the bias-fused output projection."""
+
+    fused_projection = True
 
     def __init__(self, *args, **kwargs):
         batch, seq_len, dtype = kwargs.get("batch"), kwargs.get("seq_len"), kwargs.get("dtype")

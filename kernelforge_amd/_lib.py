@@ -55,6 +55,10 @@ SIGNATURES = {
         _int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p]),
     "kf_proj_gemm": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p]),
+    "kf_litela_fused_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "kf_litela_fused_attn": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
+               _c_void_p]),
     "kf_rope_packed": (_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _int, _c_void_p]),
     "kf_fa_fwd": (
         _int,
@@ -87,6 +91,7 @@ SIGNATURES = {
 MEASURE_SIGNATURES = {
     "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _c_void_p]),
     "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
+    "kfm_litela_fused_heads": (_int, [_int]),
 }
 
 _lock = threading.Lock()

@@ -260,3 +260,38 @@ def test_grouped_full64_module_and_selector():
     _close(got, _module_ref(m, x, False))
     with pytest.raises(ValueError, match="rotary_emb=None"):
         m(x, rotary_emb=_rope_tables(N, 32))
+
+
+@pytest.mark.parametrize("use_bias", (False, True))
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
+def test_fused_projection_path_matches_reference(use_bias, dtype):
+    """LiteLA with the fused projection + attention kernels forced
+    (fused_projection=True) against the oracle and the unfused module path."""
+    torch.manual_seed(0)
+    B, N, C = 2, 300, 6 * 32
+    m = LiteLA(C, C, use_bias=use_bias).to(DEV, dtype)
+    x = torch.randn(B, N, C, generator=torch.Generator().manual_seed(8)).to(dtype).to(DEV)
+    m.fused_projection = True
+    fused = m(x)
+    m.fused_projection = False
+    unfused = m(x)
+    _close(fused, _module_ref(m, x, False))
+    _close(fused, unfused.cpu().float(), tol=1e-2)
+
+
+def test_fused_projection_path_in_a_graph():
+    """The fused path captured in a HIP graph: replays with eager work between
+    them match the eager result."""
+    B, N, C = 1, 512, 1152
+    ref, _ = _joint_pair(JointLiteLA, B, N, C, False)
+    ref.fused_projection = True
+    g = CUDAGraphJointLiteLA(ref)
+    gen = torch.Generator().manual_seed(9)
+    xs = [torch.randn(B, N, C, generator=gen).to(torch.bfloat16).to(DEV) for _ in range(2)]
+    for x in xs + xs:
+        out = g(x).clone()
+        torch.cuda.synchronize()
+        with torch.inference_mode():
+            eager = ref(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
