@@ -288,9 +288,9 @@ def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
 
 
 def bench_mfma(warmup: int) -> dict:
-    """Dense bf16 MFMA ceiling: kfm_mfma_bf16 (four independent
-    v_mfma_f32_16x16x32_bf16 chains per wavefront) at 1, 2 and 4 wavefronts
-    per SIMD, each run ~2 ms; the best rate."""
+    """Dense bf16 MFMA ceiling: kfm_mfma_bf16 (two independent
+    v_mfma_f32_32x32x16_bf16 chains per wavefront) at 1, 2 and 4 wavefronts
+    per SIMD, each run ~1-2 ms; the best rate."""
     from kernelforge_amd import _lib
 
     lib = _lib.load()
@@ -308,10 +308,10 @@ def bench_mfma(warmup: int) -> dict:
                 _lib.check(rc, "kfm_mfma_bf16")
 
         us, _ = _time_launches(launch, 1, 5, warmup)
-        flops = blocks * 4 * iters * 4 * 16384
+        flops = blocks * 4 * iters * 2 * 32768
         tflops = flops / (us * 1e-6) / 1e12
         if best is None or tflops > best["tflops"]:
-            best = dict(kernel="mfma_kernel", workload="mfma_bf16_16x16x32_dense", waves_per_simd=waves_per_simd,
+            best = dict(kernel="mfma_kernel", workload="mfma_bf16_32x32x16_dense", waves_per_simd=waves_per_simd,
                         us=us, flops=flops, tflops=tflops, frac_of_peak=tflops / BF16_PEAK_TFLOPS)
     return best
 

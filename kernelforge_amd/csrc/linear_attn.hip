@@ -396,8 +396,12 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
     // completed before their writers arrived, and no cache holds a line of
     // them from before the barrier (nothing reads them earlier in a launch,
     // and caches start every launch invalidated).
+    // The sums keep 36-float rows in LDS: the operand reads below take row
+    // m16 = 0..15 at one column in 16 lanes, which 32-float rows would put on
+    // eight banks; 36 spreads them over all 64.
+    constexpr int kRowPad = kD + 4, kPadState = (kD + 1) * kRowPad;
     float* sums = reinterpret_cast<float*>(lds + 2 * Q_BYTES);
-    static_assert(2 * Q_BYTES + 2 * kState * 4 <= LDS_BYTES, "state sums fit");
+    static_assert(2 * Q_BYTES + 2 * kPadState * 4 <= LDS_BYTES, "state sums fit");
     {
         constexpr int NV = 2 * kState / 4;  // 16-byte vectors of the pair's state
         const float* P0 = p.partial + (int64_t)(b * H + h0) * p.S * kState;
@@ -415,7 +419,8 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
 #pragma unroll
                 for (int j = 0; j < 8; ++j) acc4 += part4[j];  // split order; padding adds zero
             }
-            *reinterpret_cast<f32x4*>(sums + e) = acc4;
+            const int hh = e >= kState, rem = e - hh * kState;  // 4 floats of one row
+            *reinterpret_cast<f32x4*>(sums + hh * kPadState + (rem / kD) * kRowPad + rem % kD) = acc4;
         }
     }
     barrier_keep_loads();
@@ -425,12 +430,12 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
     const int m16 = lane & 15, kg = lane >> 4;
     float sv[2][8], zv[8];
     {
-        const float* S0 = sums + hw * kState;
+        const float* S0 = sums + hw * kPadState;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            sv[0][j] = S0[m16 * kD + 8 * kg + j];
-            sv[1][j] = S0[(16 + m16) * kD + 8 * kg + j];
-            zv[j] = S0[kD * kD + 8 * kg + j];
+            sv[0][j] = S0[m16 * kRowPad + 8 * kg + j];
+            sv[1][j] = S0[(16 + m16) * kRowPad + 8 * kg + j];
+            zv[j] = S0[kD * kRowPad + 8 * kg + j];
         }
     }
     // fp16 has a narrow exponent range: rescale the whole state by a power of
