@@ -182,7 +182,12 @@ int kf_linattn_workspace_init(void* workspace, int64_t workspace_bytes, kf_strea
  * path.  splits <= 0 selects kf_linattn_default_splits.
  * workspace: at least kf_linattn_workspace_bytes bytes, 256-byte aligned,
  * control words zero on entry (kf_linattn_workspace_init); they are zero
- * again on return.
+ * again on return.  The split workgroups of a group wait for each other a
+ * bounded time (about a quarter second); should other work on the device keep
+ * some of them from being resident that long, the ones that stop waiting set
+ * the workspace's error word (the second 32-bit control word) to 1 and write
+ * NaN for their tokens instead of a result, and the word stays set until the
+ * next kf_linattn_workspace_init.
  */
 int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
                    int64_t workspace_bytes, int64_t batch, int64_t seq_len,

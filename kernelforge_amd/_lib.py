@@ -86,12 +86,14 @@ SIGNATURES = {
     ),
 }
 
-# Measurement kernels (kernelforge_amd/csrc/measure.hip): exported by the
-# library for bench.py's ceilings, not part of the public header.
+# Measurement kernels (kernelforge_amd/csrc/measure.hip) and test hooks:
+# exported by the library for bench.py's ceilings and the tests, not part of
+# the public header.
 MEASURE_SIGNATURES = {
     "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _c_void_p]),
     "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
     "kfm_litela_fused_heads": (_int, [_int]),
+    "kfm_linattn_spin_limit": (_int, [_i64]),
 }
 
 _lock = threading.Lock()

@@ -42,6 +42,9 @@ constexpr int KV_RING = 3;
 constexpr int Q_RING = 3;
 constexpr int kOutTokens = 64;      // tokens per output workgroup of the generic path
 constexpr int kSpinLimit = 1 << 20; // polls of the group counter before giving up
+// The limit the launches pass; only the test hook kfm_linattn_spin_limit
+// changes it, to drive the give-up path from the host.
+int g_spin_limit = kSpinLimit;
 
 // --------------------------------------------------------------------------
 // Control words at the start of the workspace (uint32):
@@ -107,6 +110,7 @@ struct FusedParams {
     int N, H, npairs, S, split_len;
     int g0;             // first group (batch * npairs + pair) of this launch
     int total;          // workgroups of this launch: groups * S
+    int spin_limit;     // polls of a group counter before a member gives up
     float eps;
 };
 
@@ -171,23 +175,26 @@ __device__ __forceinline__ void store8_lds(unsigned char* tile, int row, int ch0
 // (batch, head pair)): every writer's partial has completed at the device
 // coherence point (device-coherent stores, then a wait for them) before the
 // workgroup barrier that precedes this call; thread 0 counts the arrival,
-// polls until all members have arrived (at most kSpinLimit polls, then it
+// polls until all members have arrived (at most `spin_limit` polls, then it
 // sets the error word and goes on, so no wave can wait forever), counts the
 // departure, and the last member to leave resets both counters to zero for
-// the next call.  The members then read the partials with plain loads (see
+// the next call.  Returns true, in every thread, when the wait gave up: the
+// partials are then incomplete and the caller writes NaN instead of a result.  The members then read the partials with plain loads (see
 // phase 2 for why they are current).  Agent-scope fences are not used: their L2 write-backs and
 // invalidations, once per workgroup, cost more than the rest of the kernel
 // on MI355X (write-backs ~67 us, invalidations ~10 us of a 37 us launch at
 // B=2, H=70, N=4096).
-__device__ __forceinline__ void group_barrier(unsigned* ctrl, int g, unsigned members) {
+__device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned members, int spin_limit,
+                                              int* late_flag) {
     if (threadIdx.x == 0) {
         unsigned* arrive = ctrl + kCtrlHeader + kCtrlStride * g;
         unsigned* depart = arrive + 1;
         __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        int polls = 0;
+        int polls = 0, late = 0;
         while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < members) {
-            if (++polls > kSpinLimit) {
+            if (++polls > spin_limit) {
                 __hip_atomic_store(ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                late = 1;
                 break;
             }
             __builtin_amdgcn_s_sleep(8);
@@ -196,8 +203,10 @@ __device__ __forceinline__ void group_barrier(unsigned* ctrl, int g, unsigned me
             __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        *late_flag = late;
     }
     __syncthreads();
+    return *late_flag != 0;
 }
 
 // --------------------------------------------------------------------------
@@ -233,6 +242,7 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
     static_assert(LDS_BYTES >= 2 * 3 * 64 * 17 * 4, "combine buffer fits");
     __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
     __shared__ int sh_ticket;
+    __shared__ int sh_late;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) {
@@ -384,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
 #pragma unroll
     for (int j = 0; j < Q_RING; ++j) q_gload<T>(qring[j], qkv, b, N, C, h0, nh, t_begin + j * kTT, t_end, tid);
     barrier_keep_loads();
-    group_barrier(p.ctrl, g, (unsigned)p.S);
+    const bool late = group_barrier(p.ctrl, g, (unsigned)p.S, p.spin_limit, &sh_late);
 
     // ---------------- Phase 2: the group's state, then the outputs --------
     // The group's partials of both heads (2 x 1056 floats, 528 16-byte
@@ -468,7 +478,9 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
         zhi[j] = hi;
         zlo[j] = (T)(x - (float)hi);
     }
-    const float eps = p.eps * scale;
+    // A member that stopped waiting holds an incomplete state: NaN rather than
+    // a silently wrong result.
+    const float eps = late ? __builtin_nanf("") : p.eps * scale;
 
     TO* __restrict__ out = static_cast<TO*>(p.out);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
@@ -726,6 +738,7 @@ int run_mfma(const void* qkv, void* out, const Workspace& ws, int B, int N, int 
     p.npairs = (H + 1) / 2;
     p.S = splits;
     p.split_len = split_len;
+    p.spin_limit = g_spin_limit;
     p.eps = eps;
     const int64_t groups = (int64_t)B * p.npairs;
     // Groups per launch: the control region holds kMaxGroupsPerLaunch groups,
@@ -929,6 +942,14 @@ extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64
 }
 
 extern "C" int64_t kf_linattn_noalloc_max_bytes(void) { return kLinattnScratchBytes; }
+
+// Test hook, not part of the public ABI: sets the polls a member of the fused
+// kernel makes at its group's counter before giving up (and writing NaN);
+// polls <= 0 restores the default.  Not thread-safe; tests only.
+extern "C" int kfm_linattn_spin_limit(int64_t polls) {
+    kf::g_spin_limit = polls <= 0 ? kf::kSpinLimit : (int)(polls < kf::kSpinLimit ? polls : kf::kSpinLimit);
+    return KF_OK;
+}
 
 extern "C" int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
                                       int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,

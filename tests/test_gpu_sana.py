@@ -150,6 +150,54 @@ def test_workspace_contract(dim):
     assert rc == 3 and b"aligned" in lib.kf_last_error()
 
 
+def test_group_wait_give_up_writes_nan():
+    """Failure handling of the fused kernel's group barrier, forced from the
+    host: with the poll limit cut to two polls (test hook), members that
+    arrive before the rest of their group stop waiting.  Each of them must
+    set the workspace's error word and write NaN for its tokens; every other
+    element must equal the normal result bit for bit.  The counters still
+    return to zero, and after the error word is cleared the next call is
+    normal again.  Every wave exits normally (no fault, no hang)."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    B, N, H, splits = 1, 2048, 4, 8
+    qkv = randn((B, N, 3, H * 32), torch.bfloat16, seed=21).to(DEV)
+    need = int(lib.kf_linattn_workspace_bytes(B, H, 32, splits))
+    ws = torch.zeros(need, device=DEV, dtype=torch.uint8)
+    stream = _lib.stream_of(ws)
+
+    def call():
+        out = torch.empty(B, N, H * 32, device=DEV, dtype=torch.float32)
+        _lib.check(lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), _lib.ptr(ws), need, B, N, H, 32, splits,
+                                      1e-15, _lib.KF_BF16, _lib.KF_F32, stream), "kf_linattn_fwd")
+        torch.cuda.synchronize()
+        return out
+
+    ref = call()
+    assert not torch.isnan(ref).any()
+    gave_up = False
+    try:
+        _lib.check(lib.kfm_linattn_spin_limit(2), "kfm_linattn_spin_limit")
+        for _ in range(5):
+            out = call()
+            ctrl = ws[:256].view(torch.int32).cpu()
+            nan = torch.isnan(out)
+            assert bool(nan.any()) == (int(ctrl[1]) == 1), (int(ctrl[1]), int(nan.sum()))
+            assert torch.equal(out[~nan], ref[~nan])
+            assert int(ctrl[0]) == 0  # the ticket counter returned to zero
+            if nan.any():
+                gave_up = True
+                # whole token rows of a head pair: a member's split, both heads
+                assert bool(nan.view(B, N, H // 2, 64).all(-1).eq(nan.view(B, N, H // 2, 64).any(-1)).all())
+                _lib.check(lib.kf_linattn_workspace_init(_lib.ptr(ws), need, stream), "kf_linattn_workspace_init")
+    finally:
+        _lib.check(lib.kfm_linattn_spin_limit(0), "kfm_linattn_spin_limit")
+    assert gave_up, "no member stopped waiting at a two-poll limit"
+    assert torch.equal(call(), ref)
+    assert int(ws[:256].view(torch.int32).cpu()[1]) == 0
+
+
 def test_graph_replay_and_streams():
     """The fused launch inside a HIP graph: replays after eager calls and
     between them give the eager bits each time (the counters return to zero
