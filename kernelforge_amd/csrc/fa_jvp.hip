@@ -231,8 +231,8 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
         const bool tan = JVP && (vs ? use_tv : use_tk);
         if constexpr (full_tile_shortcut<DP>()) {
             if (dense_rows && k0 + kBK <= p.Nk) {
-                load_tile_full<T, DP>(d0, s0, kv_row_stride, voff, wave);
-                if (tan) load_tile_full<T, DP>(d1, s1, kv_row_stride, voff, wave);
+                load_tile_full<T, DP, FaTile<DP>::WAVES, JVP>(d0, s0, kv_row_stride, voff, wave);
+                if (tan) load_tile_full<T, DP, FaTile<DP>::WAVES, JVP>(d1, s1, kv_row_stride, voff, wave);
                 return;
             }
         }
