@@ -43,9 +43,9 @@ struct FaBwdParams {
     float* ws_lse2;   // [B][Hq][nq_pad]: LSE * log2(e), +inf for rows >= Nq
     float* ws_delta;  // [B][Hq][nq_pad]: Delta, 0 for rows >= Nq
     int B, Nq, Nk, Hq, Hkv, D, group;
-    int n_qtiles;  // query tiles of FaTile::BQ rows (dq grid)
+    int n_qtiles;  // query tiles of dq_rows() rows (dq grid)
     int n_ktiles;  // key tiles of FaTile::BQ keys (dkdv grid)
-    int nq_pad;    // n_qtiles * FaTile::BQ
+    int nq_pad;    // query rows padded to a multiple of FaTile::BQ
     float scale;
     float scale_log2;
     int causal;
@@ -70,11 +70,18 @@ __device__ __forceinline__ typename V<T>::x8 load_row8(const T* p, bool ok) {
 // ---------------------------------------------------------------------------
 // dQ (and the per-row Delta / LSE*log2e workspace).
 // ---------------------------------------------------------------------------
+// Row blocks of 16 query rows per wavefront: two up to D = 128 (a 256-row
+// workgroup), so that every K row and K^T / V operand read from LDS feeds two
+// MFMAs and each tile copy serves twice the rows; one at D = 256.
+template <int DP> constexpr int dq_row_blocks() { return DP <= 128 ? 2 : 1; }
+template <int DP> constexpr int dq_rows() { return FaTile<DP>::BQ * dq_row_blocks<DP>(); }
+
 template <typename T, int DP>
 __global__ __launch_bounds__(FaTile<DP>::THREADS)
 __attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
 void fa_bwd_dq_kernel(const FaBwdParams p) {
-    constexpr int kBQ = FaTile<DP>::BQ, kBK = FaTile<DP>::BK;
+    constexpr int R = dq_row_blocks<DP>();
+    constexpr int kBQ = dq_rows<DP>(), kBK = FaTile<DP>::BK;
     constexpr int DS = DP / 32, DB = DP / 16;
     typedef typename V<T>::x8 x8;
     // Double-buffered K and V tiles, one LDS variable per buffer so that the
@@ -102,43 +109,53 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
     if (p.causal) qtile = p.n_qtiles - 1 - qtile;  // longest scans first
     const int hk = hq / p.group;
 
-    const int q0w = qtile * kBQ + wave * 16;
-    const int qr = q0w + (lane & 15);
-    const bool row_ok = qr < p.Nq;
+    const int q0w = qtile * kBQ + wave * 16 * R;  // first row of this wavefront
     const int64_t q_row_stride = (int64_t)p.Hq * p.D;
     const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
-    const int64_t q_off = ((int64_t)b * p.Nq + qr) * q_row_stride + (int64_t)hq * p.D;
     const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
     const int diag = p.Nk - p.Nq;
+    const float c = p.scale_log2;
 
-    // Q and dO as B operands (lane: row qr, d = 32*ds + 8*grp + 0..7), and
-    // this lane's share of Delta = dO . O.
-    x8 qreg[DS], doreg[DS];
-    float dot = 0.f;
+    // Per row block rb: this lane's row, Q and dO as B operands (d = 32*ds +
+    // 8*grp + 0..7), Delta = dO . O and LSE*log2e.
+    int qr[R], klim[R];
+    bool row_ok[R];
+    int64_t q_off[R];
+    x8 qreg[R][DS], doreg[R][DS];
+    float delta[R], nlse2[R];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-        const int d = 32 * ds + 8 * grp;
-        const bool ok = row_ok && d < p.D;
-        qreg[ds] = load_row8(static_cast<const T*>(p.q) + q_off + d, ok);
-        doreg[ds] = load_row8(static_cast<const T*>(p.dout) + q_off + d, ok);
-        const x8 ov = load_row8(static_cast<const T*>(p.o) + q_off + d, ok);
+    for (int rb = 0; rb < R; ++rb) {
+        qr[rb] = q0w + 16 * rb + (lane & 15);
+        row_ok[rb] = qr[rb] < p.Nq;
+        q_off[rb] = ((int64_t)b * p.Nq + qr[rb]) * q_row_stride + (int64_t)hq * p.D;
+        float dot = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dot = fmaf((float)doreg[ds][j], (float)ov[j], dot);
-    }
-    const float delta = row_sum4(dot);
-    const float lse2 = row_ok ? p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr] * kLog2e : __builtin_inff();
-    if (grp == 0) {
-        const int64_t w = ((int64_t)b * p.Hq + hq) * p.nq_pad + qr;
-        p.ws_lse2[w] = lse2;
-        p.ws_delta[w] = delta;
+        for (int ds = 0; ds < DS; ++ds) {
+            const int d = 32 * ds + 8 * grp;
+            const bool ok = row_ok[rb] && d < p.D;
+            qreg[rb][ds] = load_row8(static_cast<const T*>(p.q) + q_off[rb] + d, ok);
+            doreg[rb][ds] = load_row8(static_cast<const T*>(p.dout) + q_off[rb] + d, ok);
+            const x8 ov = load_row8(static_cast<const T*>(p.o) + q_off[rb] + d, ok);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) dot = fmaf((float)doreg[rb][ds][j], (float)ov[j], dot);
+        }
+        delta[rb] = row_sum4(dot);
+        const float lse2 =
+            row_ok[rb] ? p.lse[((int64_t)b * p.Hq + hq) * p.Nq + qr[rb]] * kLog2e : __builtin_inff();
+        nlse2[rb] = -lse2;
+        // The workspace holds nq_pad rows: every row the dK/dV kernel's
+        // 64-row tiles read (rows >= Nq get LSE = +inf, Delta = 0).
+        if (grp == 0 && qr[rb] < p.nq_pad) {
+            const int64_t w = ((int64_t)b * p.Hq + hq) * p.nq_pad + qr[rb];
+            p.ws_lse2[w] = lse2;
+            p.ws_delta[w] = delta[rb];
+        }
+        klim[rb] = p.causal ? min(p.Nk - 1, qr[rb] + diag) : p.Nk - 1;
     }
 
     int key_stop = p.Nk;
     if (p.causal) key_stop = min(p.Nk, max(0, qtile * kBQ + kBQ + diag));
     const int ntiles = (key_stop + kBK - 1) / kBK;
-    const int klim = p.causal ? min(p.Nk - 1, qr + diag) : p.Nk - 1;
-    const float c = p.scale_log2;
-    const float nlse2 = -lse2;
 
     const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane) : 0u;
     const bool dense_rows = p.D == DP;
@@ -158,9 +175,11 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
         load_tile<T, DP>(dst, src, kv_row_stride, p.Nk - k0, p.D, wave, lane);
     };
 
-    f32x4 dq[DB];
+    f32x4 dq[R][DB];
 #pragma unroll
-    for (int db = 0; db < DB; ++db) dq[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) dq[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
     // Operand rings (slot st % NR holds step st), as in the forward kernel;
     // the fences are left out at D = 256, whose register budget is tighter.
     constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
@@ -182,7 +201,7 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
         }
 #pragma unroll
         for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
-            f32x4 s[2], dp[2];
+            f32x4 s[R][2], dp[R][2];
             // K and V rows for step st = (key block i2, K-step ds), read PF
             // steps ahead of their MFMAs.
             auto kv_load = [&](int st) {
@@ -192,10 +211,12 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
             };
             // dP^T accumulates onto -Delta, so it ends as dP - Delta.
 #pragma unroll
-            for (int i2 = 0; i2 < 2; ++i2) {
-                s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                dp[i2] = f32x4{-delta, -delta, -delta, -delta};
-            }
+            for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2) {
+                    s[rb][i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    dp[rb][i2] = f32x4{-delta[rb], -delta[rb], -delta[rb], -delta[rb]};
+                }
 #pragma unroll
             for (int st = 0; st < PF && st < NSTEP; ++st) kv_load(st);
 #pragma unroll
@@ -203,38 +224,46 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
                 if (st + PF < NSTEP) kv_load(st + PF);
                 if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
                 const int i2 = st / DS, ds = st % DS;
-                s[i2] = mfma16x16x32(kring[st % NR], qreg[ds], s[i2]);
-                dp[i2] = mfma16x16x32(vring[st % NR], doreg[ds], dp[i2]);
+#pragma unroll
+                for (int rb = 0; rb < R; ++rb) {
+                    s[rb][i2] = mfma16x16x32(kring[st % NR], qreg[rb][ds], s[rb][i2]);
+                    dp[rb][i2] = mfma16x16x32(vring[st % NR], doreg[rb][ds], dp[rb][i2]);
+                }
                 if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
             }
             // First K^T operands of the dQ product, in flight during the
             // softmax arithmetic.
 #pragma unroll
             for (int db = 0; db < PF && db < DB; ++db) kring[db % NR] = vt_operand<T, DP>(Kt, h, db, lane);
-            if (masked) {
+            // dS = P (dP - Delta), packed to 16 bits as the B operand of
+            // dQ^T += K^T dS^T (keys 4*grp+0..3 of blocks 2h, 2h+1).
+            x8 sb[R];
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb) {
+                if (masked) {
+#pragma unroll
+                    for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (k0 + 16 * (2 * h + i2) + 4 * grp + i > klim[rb]) s[rb][i2][i] = -__builtin_inff();
+                }
+                u32x2 sw[2];
 #pragma unroll
                 for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (k0 + 16 * (2 * h + i2) + 4 * grp + i > klim) s[i2][i] = -__builtin_inff();
+                    for (int j = 0; j < 2; ++j) {
+                        const float p0 = fast_exp2(fmaf(s[rb][i2][2 * j], c, nlse2[rb]));
+                        const float p1 = fast_exp2(fmaf(s[rb][i2][2 * j + 1], c, nlse2[rb]));
+                        sw[i2][j] = Pk<T>::cvt(p0 * dp[rb][i2][2 * j], p1 * dp[rb][i2][2 * j + 1]);
+                    }
+                sb[rb] = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
             }
-            // dS = P (dP - Delta), packed to 16 bits as the B operand of
-            // dQ^T += K^T dS^T (keys 4*grp+0..3 of blocks 2h, 2h+1).
-            u32x2 sw[2];
-#pragma unroll
-            for (int i2 = 0; i2 < 2; ++i2)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float p0 = fast_exp2(fmaf(s[i2][2 * j], c, nlse2));
-                    const float p1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nlse2));
-                    sw[i2][j] = Pk<T>::cvt(p0 * dp[i2][2 * j], p1 * dp[i2][2 * j + 1]);
-                }
-            const x8 sb = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
                 if (db + PF < DB) kring[(db + PF) % NR] = vt_operand<T, DP>(Kt, h, db + PF, lane);
                 if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
-                dq[db] = mfma16x16x32(kring[db % NR], sb, dq[db]);
+#pragma unroll
+                for (int rb = 0; rb < R; ++rb) dq[rb][db] = mfma16x16x32(kring[db % NR], sb[rb], dq[rb][db]);
                 if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -249,15 +278,18 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
     }
 
     // dQ = scale * dS K; lane holds row qr, d = 16*db + 4*grp + 0..3.
-    T* const dqrow = static_cast<T*>(p.dq) + q_off;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-        const int d = 16 * db + 4 * grp;
-        if (row_ok && d < p.D) {
-            typename V<T>::x4 r;
+    for (int rb = 0; rb < R; ++rb) {
+        T* const dqrow = static_cast<T*>(p.dq) + q_off[rb];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = (T)(dq[db][e] * p.scale);
-            *reinterpret_cast<typename V<T>::x4*>(dqrow + d) = r;
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + 4 * grp;
+            if (row_ok[rb] && d < p.D) {
+                typename V<T>::x4 r;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r[e] = (T)(dq[rb][db][e] * p.scale);
+                *reinterpret_cast<typename V<T>::x4*>(dqrow + d) = r;
+            }
         }
     }
 }
@@ -572,7 +604,8 @@ extern "C" int kf_fa_bwd(const void* q, const void* k, const void* v, const void
     p.group = (int)(Hq / Hkv);
     const int dp = D <= 32 ? 32 : D <= 64 ? 64 : D <= 128 ? 128 : 256;
     const int bq = dp > 128 ? FaTile<256>::BQ : FaTile<128>::BQ;
-    p.n_qtiles = (int)((Nq + bq - 1) / bq);
+    const int bq_dq = dp > 128 ? dq_rows<256>() : dq_rows<128>();
+    p.n_qtiles = (int)((Nq + bq_dq - 1) / bq_dq);
     p.n_ktiles = (int)((Nk + bq - 1) / bq);
     p.nq_pad = (int)nq_pad;
     p.scale = scale;
