@@ -478,7 +478,14 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
                 }
                 probs(rb, s[rb], ts[rb], ew[rb], hw[rb]);
             }
+            // The wavefront entering its P.V products takes issue priority
+            // over the other wavefront of its SIMD (in its softmax arithmetic
+            // or score products), so that the MFMA pipe refills first:
+            // 0.6-1.1% faster for the JVP modes at B=2, H=16, N=4096,
+            // D=128 on MI355X (the forward saw no gain).
+            if constexpr (JVP) __builtin_amdgcn_s_setprio(1);
             pv(bufc, h, ew, hw);
+            if constexpr (JVP) __builtin_amdgcn_s_setprio(0);
         }
     };
     if (ntiles > 0) {
