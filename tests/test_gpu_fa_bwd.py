@@ -42,6 +42,10 @@ CASES = (
     (1, 64, 256, 1, 1, 136, False, None),
     (1, 200, 200, 4, 2, 256, False, None),
     (1, 300, 300, 8, 1, 128, True, None),
+    # D = 128, no mask, whole tiles: the 32-key-wavefront dK/dV kernel (GQA, MQA).
+    (1, 128, 256, 4, 2, 128, False, None),
+    (2, 192, 128, 2, 2, 128, False, 0.1),
+    (1, 64, 384, 3, 1, 128, False, None),
 )
 
 
