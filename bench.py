@@ -335,6 +335,79 @@ def bench_mfma(warmup: int) -> dict:
     return best
 
 
+def bench_coissue(warmup: int) -> dict:
+    """How much of a wavefront's own VALU work issues under its MFMAs:
+    kfm_coissue at one wavefront per SIMD (one 256-thread block per CU), two
+    independent v_mfma_f32_32x32x16_bf16 chains with K = 0..8 independent
+    v_fma_f32 or v_exp_f32 after each MFMA, and one dependent chain with no
+    VALU work ("one_chain").  Cycles come from the shader clock inside the
+    kernel (median over wavefronts); extra_cycles_per_valu =
+    (cycles_K - cycles_0) / K per MFMA."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 4096  # x 8 MFMAs per wavefront
+    out = torch.empty(cus * 256, device="cuda", dtype=torch.float32)
+    cyc = torch.zeros(cus * 4, device="cuda", dtype=torch.int64)
+    stream = _lib.stream_of(out)
+    res = dict(kernel="coissue_kernel", workload="mfma32x32x16_plus_valu", waves_per_simd=1,
+               mfma_per_wave=8 * iters)
+
+    def run(k, exp, chains):
+        def launch(_):
+            rc = lib.kfm_coissue(_lib.ptr(out), _lib.ptr(cyc), cus, iters, k, exp, chains, stream)
+            if rc:
+                _lib.check(rc, "kfm_coissue")
+
+        us, _ = _time_launches(launch, 1, 5, warmup)
+        c = cyc.double().median().item() / (8 * iters)
+        return dict(cycles_per_mfma=round(c, 2), ns_per_mfma=round(us * 1e3 / (8 * iters), 3),
+                    clock_ghz=round(c / (us * 1e3 / (8 * iters)), 3))
+
+    res["one_chain"] = run(0, 0, 1)
+    for kind, exp in (("fma", 0), ("exp", 1)):
+        rows = {k: run(k, exp, 2) for k in (0, 1, 2, 3, 4, 6, 8)}
+        for k in rows:
+            rows[k]["extra_cycles_per_valu"] = (round((rows[k]["cycles_per_mfma"] - rows[0]["cycles_per_mfma"]) / k, 2)
+                                                if k else None)
+        res[kind] = {str(k): v for k, v in rows.items()}
+    res["us"] = res["fma"]["0"]["ns_per_mfma"] * 8 * iters / 1e3
+    return res
+
+
+def bench_lds_rate(warmup: int) -> dict:
+    """LDS read issue rate per CU: kfm_lds_rate with 4, 8 and 16 wavefronts per
+    CU (one block per CU), conflict-free ds_read_b128 against
+    ds_read_b64_tr_b16.  cycles_per_instr_per_cu = the slowest wavefront's
+    shader-clock cycles (median over blocks) / the block's read instructions."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 2048
+    res = dict(kernel="lds_rate_kernel", workload="lds_reads_conflict_free")
+    for waves in (4, 8, 16):
+        out = torch.empty(cus * 64 * waves, device="cuda", dtype=torch.int32)
+        cyc = torch.zeros(cus * waves, device="cuda", dtype=torch.int64)
+        stream = _lib.stream_of(out)
+        for name, tr, nbytes in (("b128", 0, 16), ("tr_b64", 1, 8)):
+            def launch(_, tr=tr):
+                rc = lib.kfm_lds_rate(_lib.ptr(out), _lib.ptr(cyc), cus, waves, iters, tr, stream)
+                if rc:
+                    _lib.check(rc, "kfm_lds_rate")
+
+            us, _ = _time_launches(launch, 1, 5, warmup)
+            c = cyc.view(cus, waves).max(dim=1).values.double().median().item()
+            instrs = waves * iters * 8
+            res[f"{name}_w{waves}"] = dict(us=round(us, 2), cycles_per_instr_per_cu=round(c / instrs, 3),
+                                           bytes_per_cycle_per_cu=round(instrs * 64 * nbytes / c, 1))
+    res["tr_over_b128_cycles_w16"] = round(res["tr_b64_w16"]["cycles_per_instr_per_cu"] /
+                                           res["b128_w16"]["cycles_per_instr_per_cu"], 3)
+    res["us"] = res["b128_w16"]["us"]
+    return res
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (oracle on the host cores, bounded sample).
 # ---------------------------------------------------------------------------
@@ -420,7 +493,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
-                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|copy2048|copy4096|copy8192|mfma), e.g. under rocprofv3")
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|copy2048|copy4096|copy8192|mfma), e.g. under "
+                         "rocprofv3, or a hardware probe (coissue|lds_rate) that the default run skips")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="GPU time of untimed launches after the warm-up steps (clock settling)")
@@ -453,8 +527,14 @@ def main() -> int:
         "copy8192": lambda: bench_copy(16384 * 8192 * 2, steps, warmup),
         "mfma": lambda: bench_mfma(warmup),
     }
+    # Hardware probes behind claims about issue rates; --only runs them, the
+    # default run does not.
+    probes = {
+        "coissue": lambda: bench_coissue(warmup),
+        "lds_rate": lambda: bench_lds_rate(warmup),
+    }
     if args.only:
-        r = runners[args.only]()
+        r = {**runners, **probes}[args.only]()
         print(json.dumps(r), flush=True)
         return 0
 

@@ -92,6 +92,8 @@ SIGNATURES = {
 MEASURE_SIGNATURES = {
     "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _c_void_p]),
     "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
+    "kfm_coissue": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _int, _c_void_p]),
+    "kfm_lds_rate": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _c_void_p]),
     "kfm_litela_fused_heads": (_int, [_int]),
     "kfm_linattn_spin_limit": (_int, [_i64]),
 }
