@@ -96,6 +96,7 @@ MEASURE_SIGNATURES = {
     "kfm_lds_rate": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _c_void_p]),
     "kfm_litela_fused_heads": (_int, [_int]),
     "kfm_linattn_spin_limit": (_int, [_i64]),
+    "kfm_fa_bwd_key_blocks": (_int, [_int]),
 }
 
 _lock = threading.Lock()

@@ -44,7 +44,7 @@ struct FaBwdParams {
     float* ws_delta;  // [B][Hq][nq_pad]: Delta, 0 for rows >= Nq
     int B, Nq, Nk, Hq, Hkv, D, group;
     int n_qtiles;  // query tiles of dq_rows() rows (dq grid)
-    int n_ktiles;  // key tiles of FaTile::BQ keys (dkdv grid)
+    int n_ktiles;  // key tiles of FaTile::BQ keys (one-block dkdv grid)
     int nq_pad;    // query rows padded to a multiple of FaTile::BQ
     float scale;
     float scale_log2;
@@ -527,6 +527,368 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Panel layout of the [64][DP] tiles of the two-block dK/dV kernel below:
+// DP/32 panels of [64 rows][32 elements] (64-byte rows); element (r, d) sits
+// in panel d/32, row r, 16-byte chunk ((d % 32) / 8) ^ pswz(r), element d % 8,
+// with pswz(r) = (r1 ^ r2 ^ r3, r2) for row bits r1..r3.  Every operand read
+// is then one per-lane base plus a compile-time offset (the row-swizzled
+// layout needs a separate lane offset per 16-byte column, which this kernel
+// has no registers for).  pswz was found by enumerating the XOR-linear maps of
+// the row bits: with it neither the 16-byte reads (16 rows at one logical
+// chunk) nor the transposing reads (rows 4g + q, 32 bytes each) meet a bank
+// conflict in any of the LDS models the row swizzle above is conflict-free
+// in: 128 banks with 32-lane passes for 16-byte reads and one pass for 8-byte
+// reads (the one the hardware counters agree with: a map that is clean only in
+// the two narrower models measured two conflict cycles per read), 64 banks
+// with 16- and 32-lane passes, and 32 banks with 8- and 16-lane passes.  One
+// copy instruction fills 16 rows of one panel (1024 contiguous LDS bytes).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int pswz(int r) {
+    const int r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1;
+    return ((r1 ^ r2 ^ r3) << 1) | r2;
+}
+
+template <typename T, int DP>
+__device__ __forceinline__ void load_panels(T* tile, const T* g, int64_t row_stride, int rows_valid, int D,
+                                            int wave, int lane) {
+    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
+    const int r16 = lane >> 2;
+    const int cs = (lane & 3) ^ pswz(r16);
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int rb = i & 3, pnl = i >> 2;
+            const int row = 16 * rb + r16;
+            const int d = 32 * pnl + 8 * cs;
+            const void* src = (row < rows_valid && d < D) ? static_cast<const void*>(g + row * row_stride + d)
+                                                           : static_cast<const void*>(g_zero16);
+            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + pnl * 64 * 32 + 16 * rb * 32)));
+        }
+    }
+}
+
+// Byte offset of the 16-byte chunk lane `lane` copies within each 16-row
+// block of a panel (the same for every copy instruction of a full tile).
+template <typename T>
+__device__ __forceinline__ uint32_t panel_lane_offset(int64_t row_stride, int lane) {
+    const int r16 = lane >> 2;
+    return (uint32_t)(((int64_t)r16 * row_stride + 8 * ((lane & 3) ^ pswz(r16))) * (int64_t)sizeof(T));
+}
+
+// A tile whose 64 rows are all valid and hold exactly DP elements: scalar
+// base per instruction plus the one lane offset.
+template <typename T, int DP>
+__device__ __forceinline__ void load_panels_full(T* tile, const T* g, int64_t row_stride, uint32_t voff, int wave) {
+    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
+    const uint32_t t0 = __builtin_amdgcn_readfirstlane(lds_addr(tile));
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int rb = i & 3, pnl = i >> 2;
+            lds_copy16_sbase(g + (int64_t)(16 * rb) * row_stride + 32 * pnl, voff,
+                             t0 + (uint32_t)((pnl * 64 * 32 + 16 * rb * 32) * sizeof(T)));
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV with two 16-key blocks per wavefront (up to D = 128): one workgroup
+// per 2 * FaTile::BQ keys of one KV head.  The one-block kernel above is bound
+// by its LDS reads: every wavefront reads the whole Q^T and dO^T tile through
+// transposing reads to feed two MFMAs per operand.  Here each such operand
+// feeds four (dV and dK of both key blocks).  The registers hold the dK and
+// dV accumulators of both blocks and the K operands of the wavefront's 32
+// keys; V of the workgroup's keys sits in LDS and each block reads its V
+// operands once per 32-row half, and the two blocks' S and dP are computed one
+// after the other so that one block's score accumulators are live at a time.
+// Its LDS tiles use the panel layout above.
+// Per key the products accumulate in the same order as in the one-block
+// kernel.
+// ---------------------------------------------------------------------------
+template <int DP> constexpr int dkdv_wide_keys() { return 2 * FaTile<DP>::BQ; }
+
+template <typename T, int DP>
+__global__ __launch_bounds__(FaTile<DP>::THREADS)
+__attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
+void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
+    static_assert(DP <= 128, "two key blocks per wavefront fit the registers up to D = 128");
+    constexpr int kBKEYS = dkdv_wide_keys<DP>();  // keys per workgroup
+    constexpr int kBR = FaTile<DP>::BK;           // query rows per tile
+    constexpr int KB = 2;                         // 16-key blocks per wavefront
+    constexpr int DS = DP / 32, DB = DP / 16;
+    typedef typename V<T>::x8 x8;
+    static_assert(FaTile<DP>::WAVES * 16 * KB == kBKEYS, "32 keys per wavefront");
+    static_assert(kBKEYS % kBR == 0, "V is copied in whole tiles");
+    static_assert(kBR == 64, "one 64-lane copy holds a tile's row statistics");
+    __shared__ __attribute__((aligned(16))) T qt0[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T qt1[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T ot0[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T ot1[kBR * DP];
+    __shared__ __attribute__((aligned(16))) T vt[kBKEYS * DP];  // V rows of the workgroup's keys
+    __shared__ __attribute__((aligned(16))) float rs0[2][64];
+    __shared__ __attribute__((aligned(16))) float rs1[2][64];
+    auto lds_tile = [&](auto bufc, auto osc) -> T* {
+        constexpr int buf = decltype(bufc)::value;
+        if constexpr (decltype(osc)::value)
+            return buf == 0 ? ot0 : ot1;
+        else
+            return buf == 0 ? qt0 : qt1;
+    };
+    auto lds_stats = [&](auto bufc, int i) -> float* {
+        return decltype(bufc)::value == 0 ? rs0[i] : rs1[i];
+    };
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = lane >> 4;
+
+    const int logical = xcd_logical_block();
+    const int n_kt = (p.Nk + kBKEYS - 1) / kBKEYS;
+    const int ktile = logical % n_kt;
+    const int rest = logical / n_kt;
+    const int hk = rest % p.Hkv, b = rest / p.Hkv;
+
+    const int k0 = ktile * kBKEYS;  // first key of the workgroup
+    const int k0w = k0 + wave * 32;  // first key of this wavefront
+    const int64_t q_row_stride = (int64_t)p.Hq * p.D;
+    const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
+    const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
+    const int diag = p.Nk - p.Nq;  // key j valid for query i iff j <= i + diag
+
+    // V rows k0 .. k0 + kBKEYS - 1 into LDS (zeros past Nk), as kBKEYS/64
+    // panel-layout tiles; the first barrier of the scan waits for them.
+#pragma unroll
+    for (int i = 0; i < kBKEYS / kBR; ++i)
+        load_panels<T, DP>(vt + i * kBR * DP,
+                           static_cast<const T*>(p.v) + kv_base + (int64_t)(k0 + i * kBR) * kv_row_stride,
+                           kv_row_stride, p.Nk - k0 - i * kBR, p.D, wave, lane);
+
+    // K as B operands (lane: key k0w + 16*kb + l%16, d = 32*ds + 8*grp + 0..7).
+    x8 kreg[KB][DS];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const int kr = k0w + 16 * kb + (lane & 15);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            const int d = 32 * ds + 8 * grp;
+            kreg[kb][ds] = load_row8(static_cast<const T*>(p.k) + kv_base + (int64_t)kr * kv_row_stride + d,
+                                     kr < p.Nk && d < p.D);
+        }
+    }
+
+    const int n_rt = (p.Nq + kBR - 1) / kBR;
+    const int rt0 = p.causal ? min(n_rt, max(0, k0 - diag) / kBR) : 0;
+    const int per_head = n_rt - rt0;
+    const int ntiles = per_head * p.group;
+    const float c = p.scale_log2;
+
+    const uint32_t voff = panel_lane_offset<T>(q_row_stride, lane);
+    const bool dense_rows = p.D == DP;
+
+    auto tile_head = [&](int u) { return u / per_head; };
+    auto tile_row0 = [&](int u) { return (rt0 + u % per_head) * kBR; };
+
+    auto issue = [&](int u, auto bufc) {
+        const int hq = hk * p.group + tile_head(u);
+        const int r0 = tile_row0(u);
+        const int64_t off = ((int64_t)b * p.Nq + r0) * q_row_stride + (int64_t)hq * p.D;
+        const T* const qsrc = static_cast<const T*>(p.q) + off;
+        const T* const osrc = static_cast<const T*>(p.dout) + off;
+        T* const qdst = lds_tile(bufc, std::false_type{});
+        T* const odst = lds_tile(bufc, std::true_type{});
+        if (dense_rows && r0 + kBR <= p.Nq) {
+            load_panels_full<T, DP>(qdst, qsrc, q_row_stride, voff, wave);
+            load_panels_full<T, DP>(odst, osrc, q_row_stride, voff, wave);
+        } else {
+            load_panels<T, DP>(qdst, qsrc, q_row_stride, p.Nq - r0, p.D, wave, lane);
+            load_panels<T, DP>(odst, osrc, q_row_stride, p.Nq - r0, p.D, wave, lane);
+        }
+        if (wave < 2) {  // 64 rows: one dword per lane
+            const float* src = (wave == 0 ? p.ws_lse2 : p.ws_delta) + ((int64_t)b * p.Hq + hq) * p.nq_pad + r0;
+            lds_copy4_sbase(src, 4u * lane, __builtin_amdgcn_readfirstlane(lds_addr(lds_stats(bufc, wave))));
+        }
+    };
+
+    f32x4 dk[KB][DB], dv[KB][DB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    // Per-lane element offsets of the operand reads in the panel layout.
+    const int j16 = lane & 15;
+    const int nat_lane = j16 * 32 + 8 * (grp ^ pswz(j16));  // row j16, logical chunk grp
+    // Transposing reads (see vt_operand): lanes 4q..4q+3 of group g address
+    // row 4g + q, elements 4*(j16 & 3) .. +3 of the 16-wide d block, whose
+    // chunk pair is the even (m = 0) or odd (m = 1) one of its panel.
+    const int trq = 4 * grp + (j16 >> 2);
+    const int tr_lane0 = trq * 32 + 8 * (((j16 >> 1) & 1) ^ pswz(trq)) + 4 * (j16 & 1);
+    const int tr_lane1 = tr_lane0 ^ 16;  // chunk pair 1: physical chunk ^ 2
+    auto nat_read = [&](const T* tile, int row16, int ds) -> x8 {  // rows row16 + j16, d = 32*ds + 8*grp
+        return *reinterpret_cast<const x8*>(tile + ds * 64 * 32 + row16 * 32 + nat_lane);
+    };
+    auto tr_read = [&](const T* tile, int kk, int db) -> x8 {  // vt_operand(tile, kk, db, lane)
+        const T* base = tile + (db >> 1) * 64 * 32 + 32 * kk * 32 + ((db & 1) ? tr_lane1 : tr_lane0);
+        const typename V<T>::x4 lo = lds_read_tr(base);
+        const typename V<T>::x4 hi = lds_read_tr(base + 16 * 32);
+        x8 r;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r[j] = lo[j];
+            r[j + 4] = hi[j];
+        }
+        return r;
+    };
+    // Operand rings: two deep for the S/dP steps (one read ahead), three for
+    // the transposed operands (two ahead); the same registers serve both.
+    constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
+    constexpr bool kFence = true;
+    x8 qring[NR], oring[NR];
+
+    auto step = [&](int u, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        const std::integral_constant<int, buf ^ 1> nbuf;
+        const int r0 = tile_row0(u);
+        const T* Qt = lds_tile(bufc, std::false_type{});
+        const T* Ot = lds_tile(bufc, std::true_type{});
+        const float* lse2v = lds_stats(bufc, 0);
+        const float* deltav = lds_stats(bufc, 1);
+        wait_vmem();
+        __syncthreads();  // tile u (and V) resident; every wavefront is done with tile u-1
+        if (u + 1 < ntiles) issue(u + 1, nbuf);
+        // Causal: a wavefront none of whose keys any row of the tile sees
+        // adds nothing (P = 0) and skips the tile.
+        if (p.causal && k0w > r0 + kBR - 1 + diag) return;
+#pragma unroll
+        for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
+            x8 pb[KB], sb[KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const int kr = k0w + 16 * kb + (lane & 15);
+                const bool masked = p.causal && k0w + 16 * kb + 15 > r0 + diag;
+                // Steps st = 2*ds + i2: both 16-row blocks of the half at one
+                // 32-wide d chunk, whose V operand is read once.
+                // V rows of this block: tile (wave*32 + 16*kb) / 64 of vt.
+                const T* const vtile = vt + ((wave * 32 + 16 * kb) / kBR) * kBR * DP;
+                const int vrow16 = (wave * 32 + 16 * kb) % kBR;
+                x8 vring[2];
+                f32x4 s[2], dp[2];
+                auto qo_load = [&](int st) {
+                    const int ds = st / 2, i2 = st % 2;
+                    const int row16 = 16 * (2 * h + i2);
+                    qring[st % 2] = nat_read(Qt, row16, ds);
+                    oring[st % 2] = nat_read(Ot, row16, ds);
+                    if (i2 == 0) vring[ds % 2] = nat_read(vtile, vrow16, ds);
+                };
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2) {
+                    const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + 16 * (2 * h + i2) + 4 * grp);
+                    s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    dp[i2] = -dl;
+                }
+                qo_load(0);
+#pragma unroll
+                for (int st = 0; st < NSTEP; ++st) {
+                    if (st + 1 < NSTEP) qo_load(st + 1);
+                    if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                    const int ds = st / 2, i2 = st % 2;
+                    s[i2] = mfma16x16x32(qring[st % 2], kreg[kb][ds], s[i2]);
+                    dp[i2] = mfma16x16x32(oring[st % 2], vring[ds % 2], dp[i2]);
+                    if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+                }
+                u32x2 pw[2], sw[2];
+                auto probs = [&](auto mkc) {
+#pragma unroll
+                    for (int i2 = 0; i2 < 2; ++i2) {
+                        const int rl = 16 * (2 * h + i2) + 4 * grp;
+                        const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
+                        float pr[4], dsv[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            float e = fast_exp2(fmaf(s[i2][i], c, -l2[i]));
+                            if constexpr (decltype(mkc)::value) {
+                                if (kr > r0 + rl + i + diag) e = 0.f;
+                            }
+                            pr[i] = e;
+                            dsv[i] = e * dp[i2][i];
+                        }
+                        pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
+                        pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
+                        sw[i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
+                        sw[i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
+                    }
+                };
+                if (masked)
+                    probs(std::true_type{});
+                else
+                    probs(std::false_type{});
+                pb[kb] = __builtin_bit_cast(x8, u32x4{pw[0][0], pw[0][1], pw[1][0], pw[1][1]});
+                sb[kb] = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
+            }
+            // dV^T += dO^T P and dK^T += Q^T dS for both key blocks: each
+            // transposed operand feeds two MFMAs.
+            auto t_load = [&](int db) {
+                oring[db % NR] = tr_read(Ot, h, db);
+                qring[db % NR] = tr_read(Qt, h, db);
+            };
+#pragma unroll
+            for (int db = 0; db < PF && db < DB; ++db) t_load(db);
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                if (db + PF < DB) t_load(db + PF);
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) {
+                    dv[kb][db] = mfma16x16x32(oring[db % NR], pb[kb], dv[kb][db]);
+                    dk[kb][db] = mfma16x16x32(qring[db % NR], sb[kb], dk[kb][db]);
+                }
+                if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_setprio(0);
+        }
+    };
+    if (ntiles > 0) issue(0, std::integral_constant<int, 0>{});
+    for (int u = 0; u < ntiles; u += 2) {
+        step(u, std::integral_constant<int, 0>{});
+        if (u + 1 < ntiles) step(u + 1, std::integral_constant<int, 1>{});
+    }
+    if (ntiles == 0) wait_vmem();  // the V copies land before the workgroup ends
+
+    // dK = scale * dS^T Q, dV = P^T dO; lane holds key k0w + 16*kb + l%16,
+    // d = 16*db + 4*grp + 0..3.  The lane index passes through an empty asm
+    // statement so that these addresses are formed here rather than shared
+    // with the K loads before the scan (which kept them live across it).
+    int lane_out = lane;
+    asm volatile("" : "+v"(lane_out));
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const int kr = k0w + 16 * kb + (lane_out & 15);
+        const int64_t kv_off = kv_base + (int64_t)kr * kv_row_stride;
+        T* const dkrow = static_cast<T*>(p.dk) + kv_off;
+        T* const dvrow = static_cast<T*>(p.dv) + kv_off;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+            const int d = 16 * db + 4 * (lane_out >> 4);
+            if (kr < p.Nk && d < p.D) {
+                typename V<T>::x4 rk, rv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    rk[e] = (T)(dk[kb][db][e] * p.scale);
+                    rv[e] = (T)dv[kb][db][e];
+                }
+                *reinterpret_cast<typename V<T>::x4*>(dkrow + d) = rk;
+                *reinterpret_cast<typename V<T>::x4*>(dvrow + d) = rv;
+            }
+        }
+    }
+}
+
 template <int DP> int64_t nq_pad_of(int64_t Nq) {
     return (Nq + FaTile<DP>::BQ - 1) / FaTile<DP>::BQ * FaTile<DP>::BQ;
 }
@@ -535,10 +897,23 @@ int64_t padded_rows(int64_t Nq, int64_t D) {
     return D > 128 ? nq_pad_of<256>(Nq) : nq_pad_of<128>(Nq);
 }
 
+// Key blocks per wavefront of the dK/dV kernel forced by kfm_fa_bwd_key_blocks
+// (tests reach both kernels with it); 0 = chosen per shape.
+int dkdv_blocks_override = 0;
+
 template <typename T, int DP>
 int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
     const int64_t qblocks = (int64_t)p.n_qtiles * p.Hq * p.B;
-    const int64_t kblocks = (int64_t)p.n_ktiles * p.Hkv * p.B;
+    int64_t kblocks = (int64_t)p.n_ktiles * p.Hkv * p.B;
+    // Two key blocks per wavefront (half the workgroups, each doing twice the
+    // work at fewer LDS reads per product) once the grid still gives every
+    // CU more than half a workgroup; both kernels run one workgroup per CU.
+    bool wide = false;
+    if constexpr (DP <= 128) {
+        const int64_t wblocks = ((int64_t)p.Nk + dkdv_wide_keys<DP>() - 1) / dkdv_wide_keys<DP>() * p.Hkv * p.B;
+        wide = dkdv_blocks_override ? dkdv_blocks_override == 2 : 2 * wblocks > device_cu_count();
+        if (wide) kblocks = wblocks;
+    }
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff) {
         set_error("fa_bwd: grid too large");
         return KF_E_UNSUPPORTED;
@@ -550,6 +925,13 @@ int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
         if (rc != KF_OK) return rc;
     }
     if (kblocks > 0) {
+        if constexpr (DP <= 128) {
+            if (wide) {
+                hipLaunchKernelGGL((fa_bwd_dkdv_wide_kernel<T, DP>), dim3((unsigned)kblocks),
+                                   dim3(FaTile<DP>::THREADS), 0, stream, p);
+                return check_launch("fa_bwd_dkdv_wide_kernel launch");
+            }
+        }
         hipLaunchKernelGGL((fa_bwd_dkdv_kernel<T, DP>), dim3((unsigned)kblocks), dim3(FaTile<DP>::THREADS), 0,
                            stream, p);
         return check_launch("fa_bwd_dkdv_kernel launch");
@@ -576,6 +958,15 @@ bool bwd_dims_fit(int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv, in
 
 }  // namespace
 }  // namespace kf
+
+// Measurement/test hook (not in the public header): force one (1) or two (2)
+// 16-key blocks per wavefront in the dK/dV kernel for head dims up to 128; 0
+// restores the per-shape choice.
+extern "C" int kfm_fa_bwd_key_blocks(int blocks) {
+    if (blocks < 0 || blocks > 2) return KF_E_INVALID;
+    kf::dkdv_blocks_override = blocks;
+    return KF_OK;
+}
 
 extern "C" int64_t kf_fa_bwd_workspace_bytes(int64_t B, int64_t Nq, int64_t Hq, int64_t D) {
     using namespace kf;

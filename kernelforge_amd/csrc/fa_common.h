@@ -46,6 +46,11 @@ __device__ __forceinline__ void lds_copy4(const void* src, uint32_t m0) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "{m0}"(m0) : "memory");
 }
 
+// 4 bytes per lane from a wavefront-uniform base plus a per-lane byte offset.
+__device__ __forceinline__ void lds_copy4_sbase(const void* sbase, uint32_t voff, uint32_t m0) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+
 // Workgroup shape per padded head dim.  Up to D = 128: 8 wavefronts x 16
 // query rows, 64-key tiles, two wavefronts per SIMD.  D = 256 doubles the Q and
 // accumulator registers per row: 4 wavefronts x 16 rows, 32-key tiles (the

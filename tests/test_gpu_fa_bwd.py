@@ -16,6 +16,7 @@ BASELINE config shape (B=2, H=16, N=4096, D=128).
 import pytest
 import torch
 
+from kernelforge_amd import _lib
 from kernelforge_amd.flash_attention_jvp import flash_attention, flash_attention_backward, flash_attention_jvp
 from oracle import fa as orc
 
@@ -89,6 +90,54 @@ def test_gradients_match_fp64(case, dtype):
         assert actual.shape == primal.shape and actual.dtype == dtype, name
         assert torch.isfinite(actual).all(), name
         torch.testing.assert_close(actual.cpu().double(), ref, **tolerance(dtype), msg=lambda m: f"{name}: {m}")
+
+
+@pytest.fixture
+def key_blocks():
+    """Sets the dK/dV kernel's 16-key blocks per wavefront through the
+    library's test hook (1 or 2; head dims up to 128) and restores the
+    per-shape choice afterwards."""
+    lib = _lib.load()
+
+    def force(blocks):
+        _lib.check(lib.kfm_fa_bwd_key_blocks(blocks), "kfm_fa_bwd_key_blocks")
+
+    yield force
+    force(0)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", [c for c in CASES if c[5] <= 128])
+def test_dkdv_kernels_agree(case, dtype, key_blocks):
+    """The two-block dK/dV kernel (32 keys per wavefront, V staged in LDS)
+    against the one-block kernel and the fp64 oracle.  Per key both add the
+    same products in the same order, so dK and dV agree exactly."""
+    print(f"dkdv kernels case={case} dtype={dtype}", flush=True)
+    q, k, v, cot = make_inputs(case, dtype, seed=7)
+    kwargs = dict(causal=case[-2], softmax_scale=case[-1])
+    key_blocks(1)
+    one = hip_grads(q, k, v, cot, **kwargs)
+    key_blocks(2)
+    two = hip_grads(q, k, v, cot, **kwargs)
+    ref = fp64_grads(q, k, v, cot, **kwargs)
+    for name, a, b, r in zip(("dq", "dk", "dv"), one, two, ref):
+        torch.testing.assert_close(b, a, atol=0, rtol=0, msg=lambda m: f"{name}: {m}")
+        torch.testing.assert_close(b.cpu().double(), r, **tolerance(dtype), msg=lambda m: f"{name}: {m}")
+
+
+def test_dkdv_two_block_kernel_long_gqa(key_blocks):
+    """Several 256-key workgroups per head with a partial last one, GQA group
+    of 4, causal and not: the two-block kernel against the one-block kernel."""
+    for causal in (False, True):
+        case = (1, 700, 1100, 8, 2, 128, causal, None)
+        print(f"dkdv long case={case}", flush=True)
+        q, k, v, cot = make_inputs(case, torch.bfloat16, seed=8)
+        key_blocks(1)
+        one = hip_grads(q, k, v, cot, causal=causal)
+        key_blocks(2)
+        two = hip_grads(q, k, v, cot, causal=causal)
+        for a, b in zip(one, two):
+            torch.testing.assert_close(b, a, atol=0, rtol=0)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
