@@ -211,7 +211,7 @@ def bench_fa(mode: str, steps: int, warmup: int, B=2, H=16, N=4096, D=128) -> di
         fnc = lib.kf_fa_bwd
         a = (P[0], P[1], P[2], P[6], P[7], _lib.ptr(dout), *(_lib.ptr(x) for x in grads), _lib.ptr(ws),
              ws_bytes, *dims)
-        gemms, executed, name = 5, 7, "fa_bwd_dq_kernel+fa_bwd_dkdv_kernel<bf16,128>"
+        gemms, executed, name = 5, 7, "fa_bwd_dq_kernel+fa_bwd_dkdv_wide_kernel<bf16,128>"
     else:
         fnc, a = lib.kf_fa_fwd, (P[0], P[1], P[2], P[6], P[7], *dims)
         gemms, executed, name = 2, 2, "fa_kernel<bf16,128,FWD>"

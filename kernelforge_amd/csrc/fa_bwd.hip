@@ -16,12 +16,15 @@
 //      and dP^T = V dO^T over K/V tiles streamed through LDS, then
 //      dQ^T += K^T dS^T with K^T read by transposing LDS reads.  It also
 //      writes Delta and LSE*log2(e) of its rows to the workspace.
-//   2. dkdv kernel, one workgroup per (key tile, batch, KV head): K and V of
-//      its keys stay in registers, lane l owns key l%16; it streams the Q and
-//      dO tiles (plus their LSE/Delta entries) of every query head of the
-//      group, in a fixed order, computes S = Q K^T and dP = dO V^T with the
-//      key as the output column, and accumulates dV^T += dO^T P and
-//      dK^T += Q^T dS with dO^T and Q^T read by transposing LDS reads.
+//   2. dkdv kernel, one workgroup per (key tile, batch, KV head), lane l
+//      owning key l%16 of each 16-key block; it streams the Q and dO tiles
+//      (plus their LSE/Delta entries) of every query head of the group, in a
+//      fixed order, computes S = Q K^T and dP = dO V^T with the key as the
+//      output column, and accumulates dV^T += dO^T P and dK^T += Q^T dS with
+//      dO^T and Q^T read by transposing LDS reads.  Up to D = 128 on grids
+//      that fill the chip, each wavefront owns two key blocks (K in
+//      registers, V in LDS), so each transposed operand feeds four MFMAs;
+//      otherwise one block, with K and V in registers.
 // Both products of the pair are v_mfma_f32_16x16x32 with the same operand
 // enumeration as the forward: the score accumulators of two 16-row blocks
 // are directly the B operand of the next product once packed to 16 bits.
