@@ -71,6 +71,107 @@ __device__ __forceinline__ typename V<T>::x8 load_row8(const T* p, bool ok) {
 }
 
 // ---------------------------------------------------------------------------
+// Panel layout of the [64][DP] LDS tiles of the backward kernels up to
+// D = 128: DP/32 panels of [64 rows][32 elements] (64-byte rows); element
+// (r, d) sits in panel d/32, row r, 16-byte chunk ((d % 32) / 8) ^ pswz(r), element d % 8,
+// with pswz(r) = (r1 ^ r2 ^ r3, r2) for row bits r1..r3.  Every operand read
+// is then one per-lane base plus a compile-time offset, where the row-swizzled
+// layout of fa_common.h needs a separate lane offset per 16-byte column (the
+// two-block dK/dV kernel has no registers for those).  pswz was found by
+// enumerating the XOR-linear maps of the row bits: with it neither the
+// 16-byte reads (16 rows at one logical chunk) nor the transposing reads
+// (rows 4g + q, 32 bytes each) meet a bank conflict in any of the LDS models
+// the row swizzle is conflict-free in: 128 banks with 32-lane passes for 16-byte reads and one pass for 8-byte
+// reads (the one the hardware counters agree with: a map that is clean only in
+// the two narrower models measured two conflict cycles per read), 64 banks
+// with 16- and 32-lane passes, and 32 banks with 8- and 16-lane passes.  One
+// copy instruction fills 16 rows of one panel (1024 contiguous LDS bytes).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int pswz(int r) {
+    const int r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1;
+    return ((r1 ^ r2 ^ r3) << 1) | r2;
+}
+
+template <typename T, int DP>
+__device__ __forceinline__ void load_panels(T* tile, const T* g, int64_t row_stride, int rows_valid, int D,
+                                            int wave, int lane) {
+    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
+    const int r16 = lane >> 2;
+    const int cs = (lane & 3) ^ pswz(r16);
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int rb = i & 3, pnl = i >> 2;
+            const int row = 16 * rb + r16;
+            const int d = 32 * pnl + 8 * cs;
+            const void* src = (row < rows_valid && d < D) ? static_cast<const void*>(g + row * row_stride + d)
+                                                           : static_cast<const void*>(g_zero16);
+            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + pnl * 64 * 32 + 16 * rb * 32)));
+        }
+    }
+}
+
+// Byte offset of the 16-byte chunk lane `lane` copies within each 16-row
+// block of a panel (the same for every copy instruction of a full tile).
+template <typename T>
+__device__ __forceinline__ uint32_t panel_lane_offset(int64_t row_stride, int lane) {
+    const int r16 = lane >> 2;
+    return (uint32_t)(((int64_t)r16 * row_stride + 8 * ((lane & 3) ^ pswz(r16))) * (int64_t)sizeof(T));
+}
+
+// A tile whose 64 rows are all valid and hold exactly DP elements: scalar
+// base per instruction plus the one lane offset.
+template <typename T, int DP>
+__device__ __forceinline__ void load_panels_full(T* tile, const T* g, int64_t row_stride, uint32_t voff, int wave) {
+    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
+    const uint32_t t0 = __builtin_amdgcn_readfirstlane(lds_addr(tile));
+#pragma unroll
+    for (int j = 0; j < (NI + W - 1) / W; ++j) {
+        const int i = wave + j * W;
+        if (NI % W == 0 || i < NI) {
+            const int rb = i & 3, pnl = i >> 2;
+            lds_copy16_sbase(g + (int64_t)(16 * rb) * row_stride + 32 * pnl, voff,
+                             t0 + (uint32_t)((pnl * 64 * 32 + 16 * rb * 32) * sizeof(T)));
+        }
+    }
+}
+
+// Per-lane element offsets of the operand reads of a panel-layout tile.
+struct PanelLane {
+    int nat;  // 16-byte read: row l%16 (plus a multiple of 16), logical chunk l/16 of a panel
+    int tr0;  // transposing read (see vt_operand): row 4g + q, even chunk pair of a panel
+    __device__ __forceinline__ explicit PanelLane(int lane) {
+        const int j16 = lane & 15, g = lane >> 4;
+        nat = j16 * 32 + 8 * (g ^ pswz(j16));
+        const int trq = 4 * g + (j16 >> 2);
+        tr0 = trq * 32 + 8 * (((j16 >> 1) & 1) ^ pswz(trq)) + 4 * (j16 & 1);
+    }
+};
+
+// row_chunk(tile, row16 + l%16, 4*ds + l/16) of a panel-layout tile.
+template <typename T>
+__device__ __forceinline__ typename V<T>::x8 panel_chunk(const T* tile, const PanelLane& pl, int row16, int ds) {
+    return *reinterpret_cast<const typename V<T>::x8*>(tile + ds * 64 * 32 + row16 * 32 + pl.nat);
+}
+
+// vt_operand(tile, kk, db, lane) of a panel-layout tile; the odd chunk pair
+// of a panel is the even one's physical chunk ^ 2 (element offset ^ 16).
+template <typename T>
+__device__ __forceinline__ typename V<T>::x8 panel_vt_operand(const T* tile, const PanelLane& pl, int kk, int db) {
+    const T* base = tile + (db >> 1) * 64 * 32 + 32 * kk * 32 + ((db & 1) ? (pl.tr0 ^ 16) : pl.tr0);
+    const typename V<T>::x4 lo = lds_read_tr(base);
+    const typename V<T>::x4 hi = lds_read_tr(base + 16 * 32);
+    typename V<T>::x8 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r[j] = lo[j];
+        r[j + 4] = hi[j];
+    }
+    return r;
+}
+
+// ---------------------------------------------------------------------------
 // dQ (and the per-row Delta / LSE*log2e workspace).
 // ---------------------------------------------------------------------------
 // Row blocks of 16 query rows per wavefront: two up to D = 128 (a 256-row
@@ -160,7 +261,13 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
     if (p.causal) key_stop = min(p.Nk, max(0, qtile * kBQ + kBQ + diag));
     const int ntiles = (key_stop + kBK - 1) / kBK;
 
-    const uint32_t voff = full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane) : 0u;
+    // Up to D = 128 the K/V tiles use the panel layout (see pswz); at D = 256
+    // the row-swizzled layout of fa_common.h.
+    constexpr bool kPanels = DP <= 128;
+    const PanelLane pl(lane);
+    const uint32_t voff = kPanels ? panel_lane_offset<T>(kv_row_stride, lane)
+                          : full_tile_shortcut<DP>() ? full_tile_lane_offset<T, DP>(kv_row_stride, wave, lane)
+                                                     : 0u;
     const bool dense_rows = p.D == DP;
     const T* const kbase = static_cast<const T*>(p.k) + kv_base;
     const T* const vbase = static_cast<const T*>(p.v) + kv_base;
@@ -169,6 +276,13 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
         const int k0 = tile * kBK;
         T* const dst = lds_tile(bufc, vsc);
         const T* const src = (decltype(vsc)::value ? vbase : kbase) + (int64_t)k0 * kv_row_stride;
+        if constexpr (kPanels) {
+            if (dense_rows && k0 + kBK <= p.Nk)
+                load_panels_full<T, DP>(dst, src, kv_row_stride, voff, wave);
+            else
+                load_panels<T, DP>(dst, src, kv_row_stride, p.Nk - k0, p.D, wave, lane);
+            return;
+        }
         if constexpr (full_tile_shortcut<DP>()) {
             if (dense_rows && k0 + kBK <= p.Nk) {
                 load_tile_full<T, DP>(dst, src, kv_row_stride, voff, wave);
@@ -208,9 +322,20 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
             // K and V rows for step st = (key block i2, K-step ds), read PF
             // steps ahead of their MFMAs.
             auto kv_load = [&](int st) {
-                const int krow = 16 * (2 * h + st / DS) + (lane & 15);
-                kring[st % NR] = row_chunk<T, DP>(Kt, krow, 4 * (st % DS) + grp);
-                vring[st % NR] = row_chunk<T, DP>(Vt, krow, 4 * (st % DS) + grp);
+                if constexpr (kPanels) {
+                    kring[st % NR] = panel_chunk(Kt, pl, 16 * (2 * h + st / DS), st % DS);
+                    vring[st % NR] = panel_chunk(Vt, pl, 16 * (2 * h + st / DS), st % DS);
+                } else {
+                    const int krow = 16 * (2 * h + st / DS) + (lane & 15);
+                    kring[st % NR] = row_chunk<T, DP>(Kt, krow, 4 * (st % DS) + grp);
+                    vring[st % NR] = row_chunk<T, DP>(Vt, krow, 4 * (st % DS) + grp);
+                }
+            };
+            auto kt_load = [&](int db) {
+                if constexpr (kPanels)
+                    kring[db % NR] = panel_vt_operand(Kt, pl, h, db);
+                else
+                    kring[db % NR] = vt_operand<T, DP>(Kt, h, db, lane);
             };
             // dP^T accumulates onto -Delta, so it ends as dP - Delta.
 #pragma unroll
@@ -237,7 +362,7 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
             // First K^T operands of the dQ product, in flight during the
             // softmax arithmetic.
 #pragma unroll
-            for (int db = 0; db < PF && db < DB; ++db) kring[db % NR] = vt_operand<T, DP>(Kt, h, db, lane);
+            for (int db = 0; db < PF && db < DB; ++db) kt_load(db);
             // dS = P (dP - Delta), packed to 16 bits as the B operand of
             // dQ^T += K^T dS^T (keys 4*grp+0..3 of blocks 2h, 2h+1).
             x8 sb[R];
@@ -267,7 +392,7 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int db = 0; db < DB; ++db) {
-                if (db + PF < DB) kring[(db + PF) % NR] = vt_operand<T, DP>(Kt, h, db + PF, lane);
+                if (db + PF < DB) kt_load(db + PF);
                 if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int rb = 0; rb < R; ++rb) dq[rb][db] = mfma16x16x32(kring[db % NR], sb[rb], dq[rb][db]);
@@ -531,73 +656,6 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Panel layout of the [64][DP] tiles of the two-block dK/dV kernel below:
-// DP/32 panels of [64 rows][32 elements] (64-byte rows); element (r, d) sits
-// in panel d/32, row r, 16-byte chunk ((d % 32) / 8) ^ pswz(r), element d % 8,
-// with pswz(r) = (r1 ^ r2 ^ r3, r2) for row bits r1..r3.  Every operand read
-// is then one per-lane base plus a compile-time offset (the row-swizzled
-// layout needs a separate lane offset per 16-byte column, which this kernel
-// has no registers for).  pswz was found by enumerating the XOR-linear maps of
-// the row bits: with it neither the 16-byte reads (16 rows at one logical
-// chunk) nor the transposing reads (rows 4g + q, 32 bytes each) meet a bank
-// conflict in any of the LDS models the row swizzle above is conflict-free
-// in: 128 banks with 32-lane passes for 16-byte reads and one pass for 8-byte
-// reads (the one the hardware counters agree with: a map that is clean only in
-// the two narrower models measured two conflict cycles per read), 64 banks
-// with 16- and 32-lane passes, and 32 banks with 8- and 16-lane passes.  One
-// copy instruction fills 16 rows of one panel (1024 contiguous LDS bytes).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int pswz(int r) {
-    const int r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1;
-    return ((r1 ^ r2 ^ r3) << 1) | r2;
-}
-
-template <typename T, int DP>
-__device__ __forceinline__ void load_panels(T* tile, const T* g, int64_t row_stride, int rows_valid, int D,
-                                            int wave, int lane) {
-    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
-    const int r16 = lane >> 2;
-    const int cs = (lane & 3) ^ pswz(r16);
-#pragma unroll
-    for (int j = 0; j < (NI + W - 1) / W; ++j) {
-        const int i = wave + j * W;
-        if (NI % W == 0 || i < NI) {
-            const int rb = i & 3, pnl = i >> 2;
-            const int row = 16 * rb + r16;
-            const int d = 32 * pnl + 8 * cs;
-            const void* src = (row < rows_valid && d < D) ? static_cast<const void*>(g + row * row_stride + d)
-                                                           : static_cast<const void*>(g_zero16);
-            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + pnl * 64 * 32 + 16 * rb * 32)));
-        }
-    }
-}
-
-// Byte offset of the 16-byte chunk lane `lane` copies within each 16-row
-// block of a panel (the same for every copy instruction of a full tile).
-template <typename T>
-__device__ __forceinline__ uint32_t panel_lane_offset(int64_t row_stride, int lane) {
-    const int r16 = lane >> 2;
-    return (uint32_t)(((int64_t)r16 * row_stride + 8 * ((lane & 3) ^ pswz(r16))) * (int64_t)sizeof(T));
-}
-
-// A tile whose 64 rows are all valid and hold exactly DP elements: scalar
-// base per instruction plus the one lane offset.
-template <typename T, int DP>
-__device__ __forceinline__ void load_panels_full(T* tile, const T* g, int64_t row_stride, uint32_t voff, int wave) {
-    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
-    const uint32_t t0 = __builtin_amdgcn_readfirstlane(lds_addr(tile));
-#pragma unroll
-    for (int j = 0; j < (NI + W - 1) / W; ++j) {
-        const int i = wave + j * W;
-        if (NI % W == 0 || i < NI) {
-            const int rb = i & 3, pnl = i >> 2;
-            lds_copy16_sbase(g + (int64_t)(16 * rb) * row_stride + 32 * pnl, voff,
-                             t0 + (uint32_t)((pnl * 64 * 32 + 16 * rb * 32) * sizeof(T)));
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // dK, dV with two 16-key blocks per wavefront (up to D = 128): one workgroup
 // per 2 * FaTile::BQ keys of one KV head.  The one-block kernel above is bound
 // by its LDS reads: every wavefront reads the whole Q^T and dO^T tile through
@@ -723,30 +781,7 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
             dk[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
             dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-    // Per-lane element offsets of the operand reads in the panel layout.
-    const int j16 = lane & 15;
-    const int nat_lane = j16 * 32 + 8 * (grp ^ pswz(j16));  // row j16, logical chunk grp
-    // Transposing reads (see vt_operand): lanes 4q..4q+3 of group g address
-    // row 4g + q, elements 4*(j16 & 3) .. +3 of the 16-wide d block, whose
-    // chunk pair is the even (m = 0) or odd (m = 1) one of its panel.
-    const int trq = 4 * grp + (j16 >> 2);
-    const int tr_lane0 = trq * 32 + 8 * (((j16 >> 1) & 1) ^ pswz(trq)) + 4 * (j16 & 1);
-    const int tr_lane1 = tr_lane0 ^ 16;  // chunk pair 1: physical chunk ^ 2
-    auto nat_read = [&](const T* tile, int row16, int ds) -> x8 {  // rows row16 + j16, d = 32*ds + 8*grp
-        return *reinterpret_cast<const x8*>(tile + ds * 64 * 32 + row16 * 32 + nat_lane);
-    };
-    auto tr_read = [&](const T* tile, int kk, int db) -> x8 {  // vt_operand(tile, kk, db, lane)
-        const T* base = tile + (db >> 1) * 64 * 32 + 32 * kk * 32 + ((db & 1) ? tr_lane1 : tr_lane0);
-        const typename V<T>::x4 lo = lds_read_tr(base);
-        const typename V<T>::x4 hi = lds_read_tr(base + 16 * 32);
-        x8 r;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r[j] = lo[j];
-            r[j + 4] = hi[j];
-        }
-        return r;
-    };
+    const PanelLane pl(lane);
     // Operand rings: two deep for the S/dP steps (one read ahead), three for
     // the transposed operands (two ahead); the same registers serve both.
     constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
@@ -784,9 +819,9 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
                 auto qo_load = [&](int st) {
                     const int ds = st / 2, i2 = st % 2;
                     const int row16 = 16 * (2 * h + i2);
-                    qring[st % 2] = nat_read(Qt, row16, ds);
-                    oring[st % 2] = nat_read(Ot, row16, ds);
-                    if (i2 == 0) vring[ds % 2] = nat_read(vtile, vrow16, ds);
+                    qring[st % 2] = panel_chunk(Qt, pl, row16, ds);
+                    oring[st % 2] = panel_chunk(Ot, pl, row16, ds);
+                    if (i2 == 0) vring[ds % 2] = panel_chunk(vtile, pl, vrow16, ds);
                 };
 #pragma unroll
                 for (int i2 = 0; i2 < 2; ++i2) {
@@ -836,8 +871,8 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
             // dV^T += dO^T P and dK^T += Q^T dS for both key blocks: each
             // transposed operand feeds two MFMAs.
             auto t_load = [&](int db) {
-                oring[db % NR] = tr_read(Ot, h, db);
-                qring[db % NR] = tr_read(Qt, h, db);
+                oring[db % NR] = panel_vt_operand(Ot, pl, h, db);
+                qring[db % NR] = panel_vt_operand(Qt, pl, h, db);
             };
 #pragma unroll
             for (int db = 0; db < PF && db < DB; ++db) t_load(db);
