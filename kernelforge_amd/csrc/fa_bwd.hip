@@ -71,107 +71,6 @@ __device__ __forceinline__ typename V<T>::x8 load_row8(const T* p, bool ok) {
 }
 
 // ---------------------------------------------------------------------------
-// Panel layout of the [64][DP] LDS tiles of the backward kernels up to
-// D = 128: DP/32 panels of [64 rows][32 elements] (64-byte rows); element
-// (r, d) sits in panel d/32, row r, 16-byte chunk ((d % 32) / 8) ^ pswz(r), element d % 8,
-// with pswz(r) = (r1 ^ r2 ^ r3, r2) for row bits r1..r3.  Every operand read
-// is then one per-lane base plus a compile-time offset, where the row-swizzled
-// layout of fa_common.h needs a separate lane offset per 16-byte column (the
-// two-block dK/dV kernel has no registers for those).  pswz was found by
-// enumerating the XOR-linear maps of the row bits: with it neither the
-// 16-byte reads (16 rows at one logical chunk) nor the transposing reads
-// (rows 4g + q, 32 bytes each) meet a bank conflict in any of the LDS models
-// the row swizzle is conflict-free in: 128 banks with 32-lane passes for 16-byte reads and one pass for 8-byte
-// reads (the one the hardware counters agree with: a map that is clean only in
-// the two narrower models measured two conflict cycles per read), 64 banks
-// with 16- and 32-lane passes, and 32 banks with 8- and 16-lane passes.  One
-// copy instruction fills 16 rows of one panel (1024 contiguous LDS bytes).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int pswz(int r) {
-    const int r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1;
-    return ((r1 ^ r2 ^ r3) << 1) | r2;
-}
-
-template <typename T, int DP>
-__device__ __forceinline__ void load_panels(T* tile, const T* g, int64_t row_stride, int rows_valid, int D,
-                                            int wave, int lane) {
-    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
-    const int r16 = lane >> 2;
-    const int cs = (lane & 3) ^ pswz(r16);
-#pragma unroll
-    for (int j = 0; j < (NI + W - 1) / W; ++j) {
-        const int i = wave + j * W;
-        if (NI % W == 0 || i < NI) {
-            const int rb = i & 3, pnl = i >> 2;
-            const int row = 16 * rb + r16;
-            const int d = 32 * pnl + 8 * cs;
-            const void* src = (row < rows_valid && d < D) ? static_cast<const void*>(g + row * row_stride + d)
-                                                           : static_cast<const void*>(g_zero16);
-            lds_copy16(src, __builtin_amdgcn_readfirstlane(lds_addr(tile + pnl * 64 * 32 + 16 * rb * 32)));
-        }
-    }
-}
-
-// Byte offset of the 16-byte chunk lane `lane` copies within each 16-row
-// block of a panel (the same for every copy instruction of a full tile).
-template <typename T>
-__device__ __forceinline__ uint32_t panel_lane_offset(int64_t row_stride, int lane) {
-    const int r16 = lane >> 2;
-    return (uint32_t)(((int64_t)r16 * row_stride + 8 * ((lane & 3) ^ pswz(r16))) * (int64_t)sizeof(T));
-}
-
-// A tile whose 64 rows are all valid and hold exactly DP elements: scalar
-// base per instruction plus the one lane offset.
-template <typename T, int DP>
-__device__ __forceinline__ void load_panels_full(T* tile, const T* g, int64_t row_stride, uint32_t voff, int wave) {
-    constexpr int NI = DP / 8, W = FaTile<DP>::WAVES;
-    const uint32_t t0 = __builtin_amdgcn_readfirstlane(lds_addr(tile));
-#pragma unroll
-    for (int j = 0; j < (NI + W - 1) / W; ++j) {
-        const int i = wave + j * W;
-        if (NI % W == 0 || i < NI) {
-            const int rb = i & 3, pnl = i >> 2;
-            lds_copy16_sbase(g + (int64_t)(16 * rb) * row_stride + 32 * pnl, voff,
-                             t0 + (uint32_t)((pnl * 64 * 32 + 16 * rb * 32) * sizeof(T)));
-        }
-    }
-}
-
-// Per-lane element offsets of the operand reads of a panel-layout tile.
-struct PanelLane {
-    int nat;  // 16-byte read: row l%16 (plus a multiple of 16), logical chunk l/16 of a panel
-    int tr0;  // transposing read (see vt_operand): row 4g + q, even chunk pair of a panel
-    __device__ __forceinline__ explicit PanelLane(int lane) {
-        const int j16 = lane & 15, g = lane >> 4;
-        nat = j16 * 32 + 8 * (g ^ pswz(j16));
-        const int trq = 4 * g + (j16 >> 2);
-        tr0 = trq * 32 + 8 * (((j16 >> 1) & 1) ^ pswz(trq)) + 4 * (j16 & 1);
-    }
-};
-
-// row_chunk(tile, row16 + l%16, 4*ds + l/16) of a panel-layout tile.
-template <typename T>
-__device__ __forceinline__ typename V<T>::x8 panel_chunk(const T* tile, const PanelLane& pl, int row16, int ds) {
-    return *reinterpret_cast<const typename V<T>::x8*>(tile + ds * 64 * 32 + row16 * 32 + pl.nat);
-}
-
-// vt_operand(tile, kk, db, lane) of a panel-layout tile; the odd chunk pair
-// of a panel is the even one's physical chunk ^ 2 (element offset ^ 16).
-template <typename T>
-__device__ __forceinline__ typename V<T>::x8 panel_vt_operand(const T* tile, const PanelLane& pl, int kk, int db) {
-    const T* base = tile + (db >> 1) * 64 * 32 + 32 * kk * 32 + ((db & 1) ? (pl.tr0 ^ 16) : pl.tr0);
-    const typename V<T>::x4 lo = lds_read_tr(base);
-    const typename V<T>::x4 hi = lds_read_tr(base + 16 * 32);
-    typename V<T>::x8 r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        r[j] = lo[j];
-        r[j + 4] = hi[j];
-    }
-    return r;
-}
-
-// ---------------------------------------------------------------------------
 // dQ (and the per-row Delta / LSE*log2e workspace).
 // ---------------------------------------------------------------------------
 // Row blocks of 16 query rows per wavefront: two up to D = 128 (a 256-row
