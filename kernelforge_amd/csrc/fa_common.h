@@ -216,9 +216,8 @@ __device__ __forceinline__ typename V<T>::x8 vt_operand(const T* tile, int kk, i
 // layout above needs a separate lane offset per 16-byte column, which the
 // compiler keeps in registers (16-35 VGPRs per kernel).  One copy instruction
 // fills 16 rows of one panel (1024 contiguous LDS bytes) from 64-byte row
-// segments, half cache lines where the row layout copies whole ones; the
-// forward kernels, whose time depends most on their copies, ran 0.5-2%
-// slower with it.  pswz was found by enumerating the XOR-linear maps of the
+// segments.  The forward kernels ran 0.5-2% slower with this layout, and
+// keep the row layout.  pswz was found by enumerating the XOR-linear maps of the
 // row bits: with it neither the 16-byte reads (16 rows at one logical chunk)
 // nor the transposing reads (rows 4g + q, 32 bytes each) meet a bank conflict
 // in any of the LDS models the row swizzle is conflict-free in: 128 banks
