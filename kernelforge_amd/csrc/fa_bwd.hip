@@ -845,10 +845,13 @@ int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
     // Two key blocks per wavefront (half the workgroups, each doing twice the
     // work at fewer LDS reads per product) once the grid still gives every
     // CU more than half a workgroup; both kernels run one workgroup per CU.
+    // Not under a causal mask: the 256-key workgroups, and the wavefronts
+    // within one, then do unequal work (B=2, H=16, N=4096, D=128 causal on
+    // MI355X: 592 against 535 us for the whole backward).
     bool wide = false;
     if constexpr (DP <= 128) {
         const int64_t wblocks = ((int64_t)p.Nk + dkdv_wide_keys<DP>() - 1) / dkdv_wide_keys<DP>() * p.Hkv * p.B;
-        wide = dkdv_blocks_override ? dkdv_blocks_override == 2 : 2 * wblocks > device_cu_count();
+        wide = dkdv_blocks_override ? dkdv_blocks_override == 2 : !p.causal && 2 * wblocks > device_cu_count();
         if (wide) kblocks = wblocks;
     }
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff) {
