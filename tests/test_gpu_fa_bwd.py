@@ -173,10 +173,13 @@ def test_jvp_vjp_duality():
     torch.testing.assert_close(lhs, rhs, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("blocks", (1, 2))
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_deterministic_and_standalone(dtype):
+def test_deterministic_and_standalone(dtype, blocks, key_blocks):
     """Repeated backward passes give identical bits (GQA group of 4 summed in a
-    fixed order), and the standalone entry point matches autograd."""
+    fixed order), and the standalone entry point matches autograd; with both
+    dK/dV kernels."""
+    key_blocks(blocks)
     case = (2, 150, 170, 8, 2, 64, False, None)
     q, k, v, cot = make_inputs(case, dtype)
     first = hip_grads(q, k, v, cot)
@@ -217,11 +220,13 @@ def test_baseline_config_backward(causal):
         assert ((actual.float() - r).norm() / r.norm()).item() < 1e-2
 
 
-def test_backward_graph_replay():
+@pytest.mark.parametrize("blocks", (1, 2))
+def test_backward_graph_replay(blocks, key_blocks):
     """The backward launches (dq and dkdv kernels, torch-allocated workspace)
     replay from a captured HIP graph with the eager result, also after the
     cotangent changes in place; the program's own eager work runs between
-    replays."""
+    replays.  Both dK/dV kernels."""
+    key_blocks(blocks)
     case = (1, 70, 90, 4, 2, 64, True, None)
     q, k, v, cot = make_inputs(case, torch.bfloat16)
     out, lse = flash_attention(q, k, v, causal=True, return_lse=True)
