@@ -51,6 +51,23 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
     assert set(_lib.SIGNATURES) == set(decls)
 
 
+def test_measurement_entry_points_are_exported_outside_the_header(lib):
+    """The measurement and test hooks (kfm_*) are exported and bound but not
+    part of the public ABI, and reject bad arguments on the host."""
+    decls = declared_functions()
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _lib.MEASURE_SIGNATURES:
+        assert name.startswith("kfm_") and hasattr(raw, name), name
+        assert name not in decls
+    KF_E_INVALID = 1
+    for bad in (-1, 3):
+        assert lib.kfm_fa_bwd_key_blocks(bad) == KF_E_INVALID
+    assert lib.kfm_fa_bwd_key_blocks(0) == 0  # the per-shape choice (the default)
+    assert lib.kfm_copy(None, None, 15, 1, None) == KF_E_INVALID
+    assert lib.kfm_coissue(None, None, 4, 1, 0, 0, 2, None) == KF_E_INVALID
+    assert lib.kfm_lds_rate(None, None, 1, 0, 1, 0, None) == KF_E_INVALID
+
+
 def test_version_and_status_strings(lib):
     assert lib.kf_abi_version() == _lib.ABI_VERSION == 1
     assert lib.kf_status_string(0) == b"KF_OK"
