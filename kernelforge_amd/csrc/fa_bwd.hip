@@ -21,10 +21,11 @@
 //      (plus their LSE/Delta entries) of every query head of the group, in a
 //      fixed order, computes S = Q K^T and dP = dO V^T with the key as the
 //      output column, and accumulates dV^T += dO^T P and dK^T += Q^T dS with
-//      dO^T and Q^T read by transposing LDS reads.  Up to D = 128 on grids
-//      that fill the chip, each wavefront owns two key blocks (K in
-//      registers, V in LDS), so each transposed operand feeds four MFMAs;
-//      otherwise one block, with K and V in registers.
+//      dO^T and Q^T read by transposing LDS reads.  Up to D = 128 on
+//      non-causal grids that fill the chip, each wavefront owns two key
+//      blocks (four at D = 32; K in registers, V in LDS), so each transposed
+//      operand feeds four (eight) MFMAs; otherwise one block, with K and V
+//      in registers.
 // Both products of the pair are v_mfma_f32_16x16x32 with the same operand
 // enumeration as the forward: the score accumulators of two 16-row blocks
 // are directly the B operand of the next product once packed to 16 bits.
@@ -555,32 +556,38 @@ void fa_bwd_dkdv_kernel(const FaBwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV with two 16-key blocks per wavefront (up to D = 128): one workgroup
-// per 2 * FaTile::BQ keys of one KV head.  The one-block kernel above is bound
-// by its LDS reads: every wavefront reads the whole Q^T and dO^T tile through
-// transposing reads to feed two MFMAs per operand.  Here each such operand
-// feeds four (dV and dK of both key blocks).  The registers hold the dK and
-// dV accumulators of both blocks and the K operands of the wavefront's 32
-// keys; V of the workgroup's keys sits in LDS and each block reads its V
-// operands once per 32-row half, and the two blocks' S and dP are computed one
-// after the other so that one block's score accumulators are live at a time.
+// dK, dV with KB 16-key blocks per wavefront (up to D = 128; KB = 2, and 4
+// at D = 32): one workgroup per 16 * KB * WAVES keys of one KV head.  The
+// one-block kernel above is bound by its LDS reads: every wavefront reads the
+// whole Q^T and dO^T tile through transposing reads to feed two MFMAs per
+// operand.  Here each such operand feeds 2 KB (dV and dK of every key
+// block).  The registers hold the dK and dV accumulators of all blocks and
+// the K operands of the wavefront's keys; V of the workgroup's keys sits in
+// LDS and each block reads its V operands once per 32-row half, and the
+// blocks' S and dP are computed one after the other so that one block's
+// score accumulators are live at a time.
 // Its LDS tiles use the panel layout above.
 // Per key the products accumulate in the same order as in the one-block
 // kernel.
 // ---------------------------------------------------------------------------
-template <int DP> constexpr int dkdv_wide_keys() { return 2 * FaTile<DP>::BQ; }
+// 16-key blocks per wavefront: four at D = 32 (7% faster than two at B=2,
+// H=16, N=4096-8192 on MI355X), two at D = 64 (three fit the registers, but
+// 384-key workgroups leave a partial round and a partial tile: 566 against
+// 474 us at N=4096) and at D = 128.
+template <int DP> constexpr int dkdv_wide_blocks() { return DP <= 32 ? 4 : 2; }
+template <int DP> constexpr int dkdv_wide_keys() { return 16 * FaTile<DP>::WAVES * dkdv_wide_blocks<DP>(); }
 
 template <typename T, int DP>
 __global__ __launch_bounds__(FaTile<DP>::THREADS)
 __attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
 void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
-    static_assert(DP <= 128, "two key blocks per wavefront fit the registers up to D = 128");
+    static_assert(DP <= 128, "several key blocks per wavefront fit the registers up to D = 128");
     constexpr int kBKEYS = dkdv_wide_keys<DP>();  // keys per workgroup
     constexpr int kBR = FaTile<DP>::BK;           // query rows per tile
-    constexpr int KB = 2;                         // 16-key blocks per wavefront
+    constexpr int KB = dkdv_wide_blocks<DP>();    // 16-key blocks per wavefront
     constexpr int DS = DP / 32, DB = DP / 16;
     typedef typename V<T>::x8 x8;
-    static_assert(FaTile<DP>::WAVES * 16 * KB == kBKEYS, "32 keys per wavefront");
+    constexpr int KW = 16 * KB;                   // keys per wavefront
     static_assert(kBKEYS % kBR == 0, "V is copied in whole tiles");
     static_assert(kBR == 64, "one 64-lane copy holds a tile's row statistics");
     __shared__ __attribute__((aligned(16))) T qt0[kBR * DP];
@@ -612,7 +619,7 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
     const int hk = rest % p.Hkv, b = rest / p.Hkv;
 
     const int k0 = ktile * kBKEYS;  // first key of the workgroup
-    const int k0w = k0 + wave * 32;  // first key of this wavefront
+    const int k0w = k0 + wave * KW;  // first key of this wavefront
     const int64_t q_row_stride = (int64_t)p.Hq * p.D;
     const int64_t kv_row_stride = (int64_t)p.Hkv * p.D;
     const int64_t kv_base = (int64_t)b * p.Nk * kv_row_stride + (int64_t)hk * p.D;
@@ -710,9 +717,9 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
                 const bool masked = p.causal && k0w + 16 * kb + 15 > r0 + diag;
                 // Steps st = 2*ds + i2: both 16-row blocks of the half at one
                 // 32-wide d chunk, whose V operand is read once.
-                // V rows of this block: tile (wave*32 + 16*kb) / 64 of vt.
-                const T* const vtile = vt + ((wave * 32 + 16 * kb) / kBR) * kBR * DP;
-                const int vrow16 = (wave * 32 + 16 * kb) % kBR;
+                // V rows of this block: tile (wave*KW + 16*kb) / 64 of vt.
+                const T* const vtile = vt + ((wave * KW + 16 * kb) / kBR) * kBR * DP;
+                const int vrow16 = (wave * KW + 16 * kb) % kBR;
                 x8 vring[2];
                 f32x4 s[2], dp[2];
                 auto qo_load = [&](int st) {
@@ -767,8 +774,8 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
                 pb[kb] = __builtin_bit_cast(x8, u32x4{pw[0][0], pw[0][1], pw[1][0], pw[1][1]});
                 sb[kb] = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
             }
-            // dV^T += dO^T P and dK^T += Q^T dS for both key blocks: each
-            // transposed operand feeds two MFMAs.
+            // dV^T += dO^T P and dK^T += Q^T dS for every key block: each
+            // transposed operand feeds KB MFMAs.
             auto t_load = [&](int db) {
                 oring[db % NR] = panel_vt_operand(Ot, pl, h, db);
                 qring[db % NR] = panel_vt_operand(Qt, pl, h, db);
