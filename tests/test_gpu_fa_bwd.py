@@ -125,11 +125,13 @@ def test_dkdv_kernels_agree(case, dtype, key_blocks):
         torch.testing.assert_close(b.cpu().double(), r, **tolerance(dtype), msg=lambda m: f"{name}: {m}")
 
 
-def test_dkdv_two_block_kernel_long_gqa(key_blocks):
-    """Several 256-key workgroups per head with a partial last one, GQA group
-    of 4, causal and not: the two-block kernel against the one-block kernel."""
+@pytest.mark.parametrize("d", (32, 64, 128))
+def test_dkdv_two_block_kernel_long_gqa(key_blocks, d):
+    """Several multi-block workgroups per head (256 keys, 512 at D = 32) with a
+    partial last one, GQA group of 4, causal and not: the multi-block kernel
+    against the one-block kernel."""
     for causal in (False, True):
-        case = (1, 700, 1100, 8, 2, 128, causal, None)
+        case = (1, 700, 1100, 8, 2, d, causal, None)
         print(f"dkdv long case={case}", flush=True)
         q, k, v, cot = make_inputs(case, torch.bfloat16, seed=8)
         key_blocks(1)
