@@ -76,20 +76,33 @@ __device__ __forceinline__ void barrier_keep_loads() {
     asm volatile("" ::: "memory");
 }
 
-// LDS byte offsets.  K/V tile: one 256-byte row per token holding the pair's
-// 64 K channels and 64 V channels; odd rows swap the K and V halves and rows
-// with bit 1 set swap the two 64-byte quarters of each half (16-byte chunk
-// index xor 4).  A 16-lane store group (one token's K and V) and a 32-lane
-// transposing read (4 consecutive tokens x 64 bytes) then touch 64 distinct
-// banks.
+// LDS byte offsets.  The swizzles below were found by enumerating the
+// XOR-linear maps of the row bits against every access pattern of the tiles,
+// in three LDS bank models: 128 banks with 32-lane passes for 16-byte
+// accesses and one pass for 8-byte ones (the model the hardware's conflict
+// counter agrees with), 64 banks with 16- and 32-lane passes, and 32 banks
+// with 8- and 16-lane passes.
+//
+// K/V tile: one 256-byte row per token holding the pair's 64 K channels and
+// 64 V channels: 16-byte chunk L = 8*part + ch/8 (part 0 = K, 1 = V) sits at
+// L ^ kvswz(tok), kvswz(t) = (t0 ^ t3, t1, t0, 0) in chunk bits 3..0.  A
+// 16-lane store group (one token's K and V) and a transposing read (rows
+// 4g + q, 8 rows x 64 bytes) meet no conflict.
+__device__ __forceinline__ int kvswz(int t) {
+    return (((t ^ (t >> 3)) & 1) << 3) | (((t >> 1) & 1) << 2) | ((t & 1) << 1);
+}
 __device__ __forceinline__ int kv_off(int tok, int part, int ch) {
-    return tok * 256 + ((part ^ (tok & 1)) << 7) + (((ch >> 3) ^ (((tok >> 1) & 1) << 2)) << 4) + (ch & 7) * 2;
+    return tok * 256 + (((8 * part + (ch >> 3)) ^ kvswz(tok)) << 4) + (ch & 7) * 2;
 }
 // q and 16-bit output tiles: 128-byte rows (the pair's 64 channels), 16-byte
-// chunk index xor (row >> 1) & 7, so 16 consecutive rows at one chunk (an
-// MFMA operand read) hit 16 distinct slots, as do 2 rows x 8 chunks (a
-// whole-line staging access).
-__device__ __forceinline__ int r128_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+// chunk index xor rswz(row) = (r0 ^ r3, r1 ^ r2, r2) in chunk bits 2..0: 16
+// consecutive rows at one chunk (an MFMA operand read), 16 rows at the chunk
+// pairs the output staging writes, and 2 rows x 8 chunks (a whole-line
+// access) meet no conflict.
+__device__ __forceinline__ int rswz(int r) {
+    return (((r ^ (r >> 3)) & 1) << 2) | ((((r >> 1) ^ (r >> 2)) & 1) << 1) | ((r >> 2) & 1);
+}
+__device__ __forceinline__ int r128_off(int row, int chunk) { return row * 128 + ((chunk ^ rswz(row)) << 4); }
 // fp32 output tile: 256-byte rows, chunk index xor (row & 15).
 __device__ __forceinline__ int r256_off(int row, int chunk) { return row * 256 + ((chunk ^ (row & 15)) << 4); }
 
