@@ -688,9 +688,12 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
             dv[kb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     const PanelLane pl(lane);
-    // Operand rings: two deep for the S/dP steps (one read ahead), three for
-    // the transposed operands (two ahead); the same registers serve both.
-    constexpr int PF = 2, NR = PF + 1, NSTEP = 2 * DS;
+    // Operand rings: two deep for the Q/dO chunks of the S/dP steps (one read
+    // ahead; the key blocks' V chunks are read at their own step, behind the
+    // S products, which keeps the kernel within 256 registers at D = 128),
+    // three for the transposed operands (two ahead); the same registers serve
+    // both.
+    constexpr int PF = 2, NR = PF + 1;
     constexpr bool kFence = true;
     x8 qring[NR], oring[NR];
 
@@ -710,69 +713,78 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
         if (p.causal && k0w > r0 + kBR - 1 + diag) return;
 #pragma unroll
         for (int h = 0; h < FaTile<DP>::HALVES; ++h) {
-            x8 pb[KB], sb[KB];
+            u32x2 pw[KB][2], sw[KB][2];
+            // One 16-row block of the half at a time: each Q/dO chunk is read
+            // once and feeds the S/dP products of every key block.
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                const int kr = k0w + 16 * kb + (lane & 15);
-                const bool masked = p.causal && k0w + 16 * kb + 15 > r0 + diag;
-                // Steps st = 2*ds + i2: both 16-row blocks of the half at one
-                // 32-wide d chunk, whose V operand is read once.
-                // V rows of this block: tile (wave*KW + 16*kb) / 64 of vt.
-                const T* const vtile = vt + ((wave * KW + 16 * kb) / kBR) * kBR * DP;
-                const int vrow16 = (wave * KW + 16 * kb) % kBR;
-                x8 vring[2];
-                f32x4 s[2], dp[2];
-                auto qo_load = [&](int st) {
-                    const int ds = st / 2, i2 = st % 2;
-                    const int row16 = 16 * (2 * h + i2);
-                    qring[st % 2] = panel_chunk(Qt, pl, row16, ds);
-                    oring[st % 2] = panel_chunk(Ot, pl, row16, ds);
-                    if (i2 == 0) vring[ds % 2] = panel_chunk(vtile, pl, vrow16, ds);
-                };
+            for (int i2 = 0; i2 < 2; ++i2) {
+                const int row16 = 16 * (2 * h + i2);
+                const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + row16 + 4 * grp);
+                f32x4 s[KB], dp[KB];
 #pragma unroll
-                for (int i2 = 0; i2 < 2; ++i2) {
-                    const f32x4 dl = *reinterpret_cast<const f32x4*>(deltav + 16 * (2 * h + i2) + 4 * grp);
-                    s[i2] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    dp[i2] = -dl;
+                for (int kb = 0; kb < KB; ++kb) {
+                    s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    dp[kb] = -dl;
                 }
+                x8 vcur[KB];
+                auto qo_load = [&](int ds) {
+                    qring[ds % 2] = panel_chunk(Qt, pl, row16, ds);
+                    oring[ds % 2] = panel_chunk(Ot, pl, row16, ds);
+                };
+                auto v_load = [&](int ds) {
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb) {
+                        const T* const vtile = vt + ((wave * KW + 16 * kb) / kBR) * kBR * DP;
+                        vcur[kb] = panel_chunk(vtile, pl, (wave * KW + 16 * kb) % kBR, ds);
+                    }
+                };
                 qo_load(0);
 #pragma unroll
-                for (int st = 0; st < NSTEP; ++st) {
-                    if (st + 1 < NSTEP) qo_load(st + 1);
+                for (int ds = 0; ds < DS; ++ds) {
+                    v_load(ds);
+                    if (ds + 1 < DS) qo_load(ds + 1);
                     if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
-                    const int ds = st / 2, i2 = st % 2;
-                    s[i2] = mfma16x16x32(qring[st % 2], kreg[kb][ds], s[i2]);
-                    dp[i2] = mfma16x16x32(oring[st % 2], vring[ds % 2], dp[i2]);
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb)
+                        s[kb] = mfma16x16x32(qring[ds % 2], kreg[kb][ds], s[kb]);
+#pragma unroll
+                    for (int kb = 0; kb < KB; ++kb)
+                        dp[kb] = mfma16x16x32(oring[ds % 2], vcur[kb], dp[kb]);
                     if constexpr (kFence) __builtin_amdgcn_sched_barrier(0);
                 }
-                u32x2 pw[2], sw[2];
-                auto probs = [&](auto mkc) {
+                const int rl = row16 + 4 * grp;
+                const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
 #pragma unroll
-                    for (int i2 = 0; i2 < 2; ++i2) {
-                        const int rl = 16 * (2 * h + i2) + 4 * grp;
-                        const f32x4 l2 = *reinterpret_cast<const f32x4*>(lse2v + rl);
+                for (int kb = 0; kb < KB; ++kb) {
+                    const int kr = k0w + 16 * kb + (lane & 15);
+                    const bool masked = p.causal && k0w + 16 * kb + 15 > r0 + diag;
+                    auto probs = [&](auto mkc) {
                         float pr[4], dsv[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            float e = fast_exp2(fmaf(s[i2][i], c, -l2[i]));
+                            float e = fast_exp2(fmaf(s[kb][i], c, -l2[i]));
                             if constexpr (decltype(mkc)::value) {
                                 if (kr > r0 + rl + i + diag) e = 0.f;
                             }
                             pr[i] = e;
-                            dsv[i] = e * dp[i2][i];
+                            dsv[i] = e * dp[kb][i];
                         }
-                        pw[i2][0] = Pk<T>::cvt(pr[0], pr[1]);
-                        pw[i2][1] = Pk<T>::cvt(pr[2], pr[3]);
-                        sw[i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
-                        sw[i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
-                    }
-                };
-                if (masked)
-                    probs(std::true_type{});
-                else
-                    probs(std::false_type{});
-                pb[kb] = __builtin_bit_cast(x8, u32x4{pw[0][0], pw[0][1], pw[1][0], pw[1][1]});
-                sb[kb] = __builtin_bit_cast(x8, u32x4{sw[0][0], sw[0][1], sw[1][0], sw[1][1]});
+                        pw[kb][i2][0] = Pk<T>::cvt(pr[0], pr[1]);
+                        pw[kb][i2][1] = Pk<T>::cvt(pr[2], pr[3]);
+                        sw[kb][i2][0] = Pk<T>::cvt(dsv[0], dsv[1]);
+                        sw[kb][i2][1] = Pk<T>::cvt(dsv[2], dsv[3]);
+                    };
+                    if (masked)
+                        probs(std::true_type{});
+                    else
+                        probs(std::false_type{});
+                }
+            }
+            x8 pb[KB], sb[KB];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                pb[kb] = __builtin_bit_cast(x8, u32x4{pw[kb][0][0], pw[kb][0][1], pw[kb][1][0], pw[kb][1][1]});
+                sb[kb] = __builtin_bit_cast(x8, u32x4{sw[kb][0][0], sw[kb][0][1], sw[kb][1][0], sw[kb][1][1]});
             }
             // dV^T += dO^T P and dK^T += Q^T dS for every key block: each
             // transposed operand feeds KB MFMAs.
