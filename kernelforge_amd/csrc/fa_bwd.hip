@@ -106,7 +106,7 @@ void fa_bwd_dq_kernel(const FaBwdParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;
 
-    const int logical = xcd_logical_block();
+    const int logical = p.causal ? causal_tile_order(xcd_logical_block(), p.n_qtiles) : xcd_logical_block();
     int qtile = logical % p.n_qtiles;
     const int rest = logical / p.n_qtiles;
     const int hq = rest % p.Hq, b = rest / p.Hq;

@@ -315,6 +315,22 @@ __device__ __forceinline__ typename V<T>::x8 panel_vt_operand(const T* tile, con
     return r;
 }
 
+// Causal grids, where a head's tiles are numbered longest first: the logical
+// block numbers of one XCD (a contiguous range, consecutive tiles of a head)
+// dealt round-robin over that range's heads, so that the XCD starts every
+// head's longest tile before any head's shorter ones (longest-processing-time
+// order; one head after another leaves the longest tiles of the last heads
+// for the end).  The XCD keeps the same heads.  Applies when every XCD range
+// holds whole heads; otherwise the order is left as it is.
+__device__ __forceinline__ int causal_tile_order(int logical, int n_tiles) {
+    const int nblk = gridDim.x;
+    if (nblk & 7) return logical;
+    const int per = nblk >> 3;
+    if (per % n_tiles) return logical;
+    const int heads = per / n_tiles, s = logical % per;
+    return logical - s + (s % heads) * n_tiles + s / heads;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Packed 16-bit pairs: round-to-nearest-even conversion of two floats and a

@@ -59,7 +59,8 @@ struct FaBlock {
 __device__ __forceinline__ FaBlock fa_block(const FaParams& p) {
     const int nblk = gridDim.x, id = blockIdx.x;
     const int per = nblk >> 3, rem = nblk & 7, xcd = id & 7, slot = id >> 3;
-    const int logical = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    const int lg = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    const int logical = p.causal ? causal_tile_order(lg, p.n_qtiles) : lg;
     FaBlock r;
     r.qtile = logical % p.n_qtiles;
     const int rest = logical / p.n_qtiles;
