@@ -21,11 +21,11 @@
 //      (plus their LSE/Delta entries) of every query head of the group, in a
 //      fixed order, computes S = Q K^T and dP = dO V^T with the key as the
 //      output column, and accumulates dV^T += dO^T P and dK^T += Q^T dS with
-//      dO^T and Q^T read by transposing LDS reads.  Up to D = 128 on
-//      non-causal grids that fill the chip, each wavefront owns two key
-//      blocks (four at D = 32; K in registers, V in LDS), so each transposed
-//      operand feeds four (eight) MFMAs; otherwise one block, with K and V
-//      in registers.
+//      dO^T and Q^T read by transposing LDS reads.  Up to D = 128 on grids
+//      that fill the chip (causal: D = 64 and 128), each wavefront owns two
+//      key blocks (four at D = 32; K in registers, V in LDS), so each
+//      transposed operand feeds four (eight) MFMAs; otherwise one block,
+//      with K and V in registers.
 // Both products of the pair are v_mfma_f32_16x16x32 with the same operand
 // enumeration as the forward: the score accumulators of two 16-row blocks
 // are directly the B operand of the next product once packed to 16 bits.
@@ -612,8 +612,8 @@ void fa_bwd_dkdv_wide_kernel(const FaBwdParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;
 
-    const int logical = xcd_logical_block();
     const int n_kt = (p.Nk + kBKEYS - 1) / kBKEYS;
+    const int logical = p.causal ? causal_tile_order(xcd_logical_block(), n_kt) : xcd_logical_block();
     const int ktile = logical % n_kt;
     const int rest = logical / n_kt;
     const int hk = rest % p.Hkv, b = rest / p.Hkv;
@@ -864,13 +864,16 @@ int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
     // Two key blocks per wavefront (half the workgroups, each doing twice the
     // work at fewer LDS reads per product) once the grid still gives every
     // CU more than half a workgroup; both kernels run one workgroup per CU.
-    // Not under a causal mask: the 256-key workgroups, and the wavefronts
-    // within one, then do unequal work (B=2, H=16, N=4096, D=128 causal on
-    // MI355X: 592 against 535 us for the whole backward).
+    // Under a causal mask, with the longest key tiles started first
+    // (causal_tile_order), it is faster at D = 128 and 64 (B=2, H=16,
+    // N=4096 on MI355X: 416 against 470 us and 258 against 296 us for the
+    // whole backward) but not at D = 32, whose 512-key workgroups and the
+    // wavefronts within one do too unequal work (245 against 229 us).
     bool wide = false;
     if constexpr (DP <= 128) {
         const int64_t wblocks = ((int64_t)p.Nk + dkdv_wide_keys<DP>() - 1) / dkdv_wide_keys<DP>() * p.Hkv * p.B;
-        wide = dkdv_blocks_override ? dkdv_blocks_override == 2 : !p.causal && 2 * wblocks > device_cu_count();
+        wide = dkdv_blocks_override ? dkdv_blocks_override == 2
+                                     : (!p.causal || DP > 32) && 2 * wblocks > device_cu_count();
         if (wide) kblocks = wblocks;
     }
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff) {
