@@ -345,7 +345,7 @@ def bench_coissue(warmup: int) -> dict:
     (cycles_K - cycles_0) / K per MFMA."""
     from kernelforge_amd import _lib
 
-    lib = _lib.load()
+    lib = _lib.load_probes()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     iters = 4096  # x 8 MFMAs per wavefront
     out = torch.empty(cus * 256, device="cuda", dtype=torch.float32)
@@ -383,7 +383,7 @@ def bench_lds_rate(warmup: int) -> dict:
     shader-clock cycles (median over blocks) / the block's read instructions."""
     from kernelforge_amd import _lib
 
-    lib = _lib.load()
+    lib = _lib.load_probes()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     iters = 2048
     res = dict(kernel="lds_rate_kernel", workload="lds_reads_conflict_free")

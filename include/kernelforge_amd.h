@@ -44,7 +44,8 @@ typedef enum kf_status {
     KF_E_INVALID = 1,     /* bad shape, dtype, pointer or argument value */
     KF_E_UNSUPPORTED = 2, /* a valid request this build has no kernel for */
     KF_E_WORKSPACE = 3,   /* workspace missing or too small */
-    KF_E_HIP = 4          /* a HIP runtime call or kernel launch failed */
+    KF_E_HIP = 4,         /* a HIP runtime call or kernel launch failed */
+    KF_E_INCOMPLETE = 5   /* a finished launch reported an incomplete result (kf_linattn_check) */
 } kf_status;
 
 /* ABI version of the loaded library (KF_ABI_VERSION at build time). */
@@ -179,20 +180,50 @@ int kf_linattn_workspace_init(void* workspace, int64_t workspace_bytes, kf_strea
  * dim must be 32 for the MFMA kernel in this build (one launch: the split
  * workgroups of a (batch, head pair) meet at a counter in the workspace's
  * control words); other head dims and fp32 input take a three-launch VALU
- * path.  splits <= 0 selects kf_linattn_default_splits.
- * workspace: at least kf_linattn_workspace_bytes bytes, 256-byte aligned,
- * control words zero on entry (kf_linattn_workspace_init); they are zero
- * again on return.  The split workgroups of a group wait for each other a
- * bounded time (about a quarter second); should other work on the device keep
- * some of them from being resident that long, the ones that stop waiting set
- * the workspace's error word (the second 32-bit control word) to 1 and write
- * NaN for their tokens instead of a result, and the word stays set until the
- * next kf_linattn_workspace_init.
+ * path.  splits <= 0 selects kf_linattn_default_splits; any positive count is
+ * accepted and used as an upper bound: it is cut to the sequence length and,
+ * for the fused kernel, to the number of its workgroups the device holds at
+ * once (occupancy per CU x CUs: 256 on MI355X for fp32 output), because a
+ * group's split workgroups wait for each other and must be resident
+ * together.  Each split then takes whole 128-token tiles (32 on the VALU
+ * path), so fewer splits than requested may run.
+ * workspace: at least kf_linattn_workspace_bytes bytes for the requested
+ * splits, 256-byte aligned, control words zero on entry
+ * (kf_linattn_workspace_init); they are zero again on return.  The split
+ * workgroups of a group wait for each other a bounded time (2^20 polls,
+ * about a second); should other work on the device keep some of them from
+ * being resident that long, the ones that stop waiting set the workspace's
+ * error word (the second 32-bit control word) to 1 and write NaN for their
+ * tokens instead of a result.  kf_linattn_check reports and clears it.
  */
 int kf_linattn_fwd(const void* qkv, void* out, void* workspace,
                    int64_t workspace_bytes, int64_t batch, int64_t seq_len,
                    int64_t heads, int64_t dim, int64_t splits, float eps,
                    int in_dtype, int out_dtype, kf_stream_t stream);
+
+/*
+ * LiteLA.attn_matmul(q, k, v)               SANA_LinearAttention/original.py:99-117
+ * for q, k, v that are the views LiteLA.forward makes of one packed buffer
+ * (original.py:122-134): the arithmetic of kf_linattn_fwd, with the result
+ * written as attn_matmul returns it, fp32 out[batch, heads, dim, seq_len]
+ * (contiguous; element (b, h, r, n) at ((b*heads + h)*dim + r)*seq_len + n).
+ * qkv, workspace and splits as for kf_linattn_fwd (in_dtype KF_BF16, KF_F16
+ * or KF_F32; head dim 32 with 16-bit input runs the fused MFMA kernel).
+ */
+int kf_linattn_attn_matmul(const void* qkv, float* out, void* workspace,
+                           int64_t workspace_bytes, int64_t batch, int64_t seq_len,
+                           int64_t heads, int64_t dim, int64_t splits, float eps,
+                           int in_dtype, kf_stream_t stream);
+
+/*
+ * Status of the SANA launches that used `workspace` since its last check:
+ * waits for `stream` (the one exception to the no-synchronisation rule, so
+ * not for use under graph capture), reads the workspace's error word and
+ * returns KF_OK, or KF_E_INCOMPLETE with a message when a group wait gave
+ * up (those outputs hold NaN) or the control words were not zero on entry;
+ * in that case the control words are cleared for the next call.
+ */
+int kf_linattn_check(void* workspace, int64_t workspace_bytes, kf_stream_t stream);
 
 /*
  * Largest scratch, in bytes, that kf_linattn_fwd_noalloc can use: the size
@@ -220,6 +251,13 @@ int64_t kf_linattn_noalloc_max_bytes(void);
 int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
                            int64_t heads, int64_t dim, int64_t splits, float eps,
                            int in_dtype, int out_dtype, kf_stream_t stream);
+
+/*
+ * kf_linattn_check for the current device's static scratch, the status of
+ * the kf_linattn_fwd_noalloc calls on it.  No counterpart in the reference;
+ * for the callers of kf_linattn_fwd_noalloc.
+ */
+int kf_linattn_noalloc_check(kf_stream_t stream);
 
 /*
  * Rotary position embedding, in place on the q and k parts of a packed

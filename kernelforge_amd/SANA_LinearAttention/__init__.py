@@ -5,10 +5,10 @@ variants (``CustomOpJointLiteLA``, ``CUDAGraphJointLiteLA``,
 ``GroupedFull64QOutLiteLA``, ``optimized_joint_litela``) and the
 ``qkv_projection`` factory."""
 
-from .custom import default_splits, linear_attention, qkv_attn_matmul
+from .custom import attn_matmul, check_status, default_splits, linear_attention, qkv_attn_matmul
 from .modules import (CUDAGraphJointLiteLA, CustomLiteLA, CustomOpJointLiteLA, GroupedFull64QOutLiteLA,
                       JointLiteLA, LiteLA, apply_rotary_emb, optimized_joint_litela, qkv_projection)
 
 __all__ = ["LiteLA", "CustomLiteLA", "apply_rotary_emb", "qkv_attn_matmul", "qkv_projection", "JointLiteLA",
            "CustomOpJointLiteLA", "CUDAGraphJointLiteLA", "optimized_joint_litela", "GroupedFull64QOutLiteLA",
-           "linear_attention", "default_splits"]
+           "linear_attention", "default_splits", "attn_matmul", "check_status"]

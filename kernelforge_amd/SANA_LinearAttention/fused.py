@@ -67,9 +67,15 @@ def prefer_fused(batch: int, seq_len: int, heads: int, device: torch.device) -> 
 
 
 def litela_fused_attention(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],
-                           heads: int, eps: float = 1e-15) -> torch.Tensor:
+                           heads: int, eps: float = 1e-15, heads_per_group: Optional[int] = None) -> torch.Tensor:
     """``x[B, N, C]`` with the packed ``qkv_weight[3C, C]`` (and ``qkv_bias[3C]``)
-    -> the attention output ``[B, N, C]`` in x's dtype, head dim 32."""
+    -> the attention output ``[B, N, C]`` in x's dtype, head dim 32.
+
+    ``heads_per_group`` (3 or 4) forces the workgroup tile's head count, which
+    is otherwise chosen per shape; the result is the same up to the fp32
+    summation order of the state."""
+    if heads_per_group not in (None, 3, 4):
+        raise ValueError(f"heads_per_group must be None, 3 or 4, got {heads_per_group}")
     if x.dim() != 3:
         raise ValueError(f"x must be [B, N, C], got {tuple(x.shape)}")
     B, N, C = x.shape
@@ -92,7 +98,11 @@ def litela_fused_attention(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: 
         return out
     nbytes = int(lib.kf_litela_fused_workspace_bytes(B, N, heads))
     ws = _workspace(x.device, nbytes)
-    rc = lib.kf_litela_fused_attn(_lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(out), _lib.ptr(ws), ws.numel(),
-                                  B, N, heads, HEAD_DIM, float(eps), _lib.kf_dtype(x.dtype), _lib.stream_of(x))
+    args = (_lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(out), _lib.ptr(ws), ws.numel(), B, N, heads, HEAD_DIM,
+            float(eps), _lib.kf_dtype(x.dtype))
+    if heads_per_group is None:
+        rc = lib.kf_litela_fused_attn(*args, _lib.stream_of(x))
+    else:
+        rc = lib.kfm_litela_fused_attn_heads(*args, heads_per_group, _lib.stream_of(x))
     _lib.check(rc, "kf_litela_fused_attn")
     return out

@@ -60,7 +60,7 @@ from torch import nn
 
 from .. import _lib
 from ..rmsnorm.custom import RMSNorm, rms_norm_rows_
-from .custom import THREADS, linear_attention
+from .custom import THREADS, attn_matmul, linear_attention
 from .fused import fused_applicable, litela_fused_attention, prefer_fused
 from .projection import TORCH_DTYPES, linear, qkv_projection  # noqa: F401  (re-exported)
 
@@ -201,6 +201,13 @@ class LiteLA(nn.Module):
         else:
             self.q_norm = nn.Identity()
             self.k_norm = nn.Identity()
+
+    def attn_matmul(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """ReLU linear attention of q ``[B, h, d, N]``, k ``[B, h, N, d]`` and v
+        ``[B, h, d, N]`` -> fp32 ``[B, h, d, N]`` (original.py:99-117), on the
+        HIP kernel with fp32 arithmetic; views of one packed qkv buffer, as
+        ``forward`` makes them, are read in place (``custom.attn_matmul``)."""
+        return attn_matmul(q, k, v, self.eps)
 
     def _norm_weights(self):
         if not self.qk_norm:

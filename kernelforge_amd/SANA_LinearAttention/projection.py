@@ -53,14 +53,14 @@ def _launch(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
     if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
         raise ValueError(f"weight and bias must have x's dtype {x.dtype}")
     _lib.require_gpu(x, weight, bias)
+    if bias is not None and bias.shape != (n,):
+        raise ValueError(f"bias must be [{n}], got {tuple(bias.shape)}")
     if n % 8 or k % 8:
-        raise ValueError(f"projection sizes must be multiples of 8 (in {k}, out {n})")
+        return _launch_padded(x, weight, bias, layout, n, out)
     weight = weight.contiguous()
     if weight.data_ptr() % 16:
         weight = weight.clone()
     if bias is not None:
-        if bias.shape != (n,):
-            raise ValueError(f"bias must be [{n}], got {tuple(bias.shape)}")
         bias = bias.contiguous()
     x2, ldx = _rows(x, k)
     if out is None:
@@ -72,6 +72,35 @@ def _launch(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
                                   layout, _lib.kf_dtype(x.dtype), _lib.stream_of(x))
     _lib.check(rc, "kf_proj_gemm")
     return out
+
+
+def _launch_padded(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], layout: int, n: int,
+                   out: Optional[torch.Tensor]) -> torch.Tensor:
+    """The GEMM for widths that are not multiples of 8 (its 16-byte operand
+    rows need them): x, the weight and the bias are copied into zero-padded
+    buffers of the next multiples of 8, the kernel runs on those, and the
+    first n output columns are kept.  The padded products are exact zeros, so
+    the result equals an unpadded GEMM's."""
+    k = x.shape[-1]
+    kp, np_ = -(-k // 8) * 8, -(-n // 8) * 8
+    xp = x.new_zeros(*x.shape[:-1], kp)
+    xp[..., :k] = x
+    if layout == _lib.KF_WEIGHT_NK:
+        wp = weight.new_zeros(np_, kp)
+        wp[:n, :k] = weight
+    else:
+        wp = weight.new_zeros(kp, np_)
+        wp[:k, :n] = weight
+    bp = None
+    if bias is not None:
+        bp = bias.new_zeros(np_)
+        bp[:n] = bias
+    y = _launch(xp, wp, bp, layout, np_, None)[..., :n]
+    if out is None:
+        return y.contiguous()
+    if out.shape != y.shape or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous tensor of the result's shape and dtype")
+    return out.copy_(y)
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,

@@ -50,9 +50,15 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int,
          _c_void_p],
     ),
+    "kf_linattn_attn_matmul": (
+        _int,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
+    ),
+    "kf_linattn_check": (_int, [_c_void_p, _i64, _c_void_p]),
     "kf_linattn_noalloc_max_bytes": (_i64, []),
     "kf_linattn_fwd_noalloc": (
         _int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _c_void_p]),
+    "kf_linattn_noalloc_check": (_int, [_c_void_p]),
     "kf_proj_gemm": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _int, _int, _c_void_p]),
     "kf_litela_fused_workspace_bytes": (_i64, [_i64, _i64, _i64]),
@@ -86,21 +92,40 @@ SIGNATURES = {
     ),
 }
 
-# Measurement kernels (kernelforge_amd/csrc/measure.hip) and test hooks:
-# exported by the library for bench.py's ceilings and the tests, not part of
-# the public header.
+# Measurement kernels (kernelforge_amd/csrc/measure.hip: bench.py's copy and
+# MFMA ceilings) and test entry points (a public entry point plus one per-call
+# argument that forces a kernel choice or a limit; no global state): exported
+# by the library, not part of the public header.
 MEASURE_SIGNATURES = {
     "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _c_void_p]),
     "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
+    "kfm_litela_fused_attn_heads": (
+        _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int,
+               _int, _c_void_p]),
+    "kfm_linattn_fwd_spin": (
+        _int,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _i64,
+         _c_void_p],
+    ),
+    "kfm_linattn_split_plan": (_int, [_i64, _i64, _i64, _i64, ctypes.POINTER(_i64)]),
+    "kfm_fa_bwd_blocks": (
+        _int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+         _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int, _int, _int, _c_void_p],
+    ),
+}
+
+# Hardware probes (kernelforge_amd/csrc/probes/), in their own library.
+PROBES_PATH = Path(__file__).resolve().parent / "libkernelforge_amd_probes.so"
+PROBE_SIGNATURES = {
     "kfm_coissue": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _int, _c_void_p]),
     "kfm_lds_rate": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _c_void_p]),
-    "kfm_litela_fused_heads": (_int, [_int]),
-    "kfm_linattn_spin_limit": (_int, [_i64]),
-    "kfm_fa_bwd_key_blocks": (_int, [_int]),
 }
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_probes: ctypes.CDLL | None = None
 
 
 def load() -> ctypes.CDLL:
@@ -125,6 +150,23 @@ def load() -> ctypes.CDLL:
                 raise RuntimeError(f"kernelforge_amd ABI mismatch: library {version}, python {ABI_VERSION}")
             _lib = lib
     return _lib
+
+
+def load_probes() -> ctypes.CDLL:
+    """Open the hardware-probe library (measurement only; bench.py --only)."""
+    global _probes
+    load()
+    with _lock:
+        if _probes is None:
+            if not PROBES_PATH.exists():
+                raise RuntimeError(f"probe library missing at {PROBES_PATH}; build with `python -m kernelforge_amd.build`")
+            lib = ctypes.CDLL(str(PROBES_PATH))
+            for name, (res, args) in PROBE_SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _probes = lib
+    return _probes
 
 
 def check(rc: int, what: str) -> None:

@@ -1,9 +1,12 @@
 """Build libkernelforge_amd.so in-tree with hipcc for gfx950.
 
-Every HIP/C++ source under ``csrc/`` is compiled to an object (in parallel)
-and linked into ``kernelforge_amd/libkernelforge_amd.so``.  The library has
-a plain C ABI (``include/kernelforge_amd.h``); Python reaches it through
-ctypes (``kernelforge_amd/_lib.py``), so no torch headers are compiled.
+Every HIP/C++ source directly under ``csrc/`` is compiled to an object (in
+parallel) and linked into ``kernelforge_amd/libkernelforge_amd.so``.  The
+library has a plain C ABI (``include/kernelforge_amd.h``); Python reaches it
+through ctypes (``kernelforge_amd/_lib.py``), so no torch headers are
+compiled.  The hardware probes under ``csrc/probes/`` (measurement code that
+bench.py runs on request) go into a library of their own,
+``kernelforge_amd/libkernelforge_amd_probes.so``.
 
 Run ``python -m kernelforge_amd.build`` (or ``__graft_entry__.build()``).
 """
@@ -22,6 +25,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libkernelforge_amd.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+PROBES_PATH = PKG_DIR / "libkernelforge_amd_probes.so"
 OBJ_DIR = PKG_DIR / "_build"
 
 ARCH = "gfx950"
@@ -50,8 +54,12 @@ def _sources() -> list[Path]:
     return sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp"))
 
 
+def _probe_sources() -> list[Path]:
+    return sorted(p for p in (CSRC / "probes").iterdir() if p.suffix == ".hip")
+
+
 def _compile(hipcc: str, src: Path, verbose: bool) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
+    obj = OBJ_DIR / (("probe_" if src.parent.name == "probes" else "") + src.stem + ".o")
     cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -66,22 +74,33 @@ def _compile(hipcc: str, src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every source in csrc/ and link the shared library; return its path."""
-    hipcc = _hipcc()
-    OBJ_DIR.mkdir(exist_ok=True)
-    sources = _sources()
-    jobs = jobs or min(len(sources), max(1, min(os.cpu_count() or 1, 16)))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(hipcc, s, verbose), sources))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _link(hipcc: str, objs: list[Path], path: Path, verbose: bool) -> None:
+    tmp = path.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every source in csrc/ and link the product library, then the
+    probes library (csrc/probes/ plus the error-reporting object); return the
+    product library's path."""
+    hipcc = _hipcc()
+    OBJ_DIR.mkdir(exist_ok=True)
+    sources = _sources()
+    probes = _probe_sources()
+    everything = sources + probes
+    jobs = jobs or min(len(everything), max(1, min(os.cpu_count() or 1, 16)))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(hipcc, s, verbose), everything))
+    main_objs, probe_objs = objs[:len(sources)], objs[len(sources):]
+    _link(hipcc, main_objs, LIB_PATH, verbose)
+    abi_obj = [o for o, src in zip(main_objs, sources) if src.name == "abi.cpp"]
+    _link(hipcc, probe_objs + abi_obj, PROBES_PATH, verbose)
     return LIB_PATH
 
 

@@ -52,6 +52,7 @@ const char* kf_status_string(int status) {
         case KF_E_UNSUPPORTED: return "KF_E_UNSUPPORTED";
         case KF_E_WORKSPACE: return "KF_E_WORKSPACE";
         case KF_E_HIP: return "KF_E_HIP";
+        case KF_E_INCOMPLETE: return "KF_E_INCOMPLETE";
         default: return "KF_E_UNKNOWN";
     }
 }

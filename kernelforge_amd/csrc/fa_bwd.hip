@@ -853,12 +853,10 @@ int64_t padded_rows(int64_t Nq, int64_t D) {
     return D > 128 ? nq_pad_of<256>(Nq) : nq_pad_of<128>(Nq);
 }
 
-// Key blocks per wavefront of the dK/dV kernel forced by kfm_fa_bwd_key_blocks
-// (tests reach both kernels with it); 0 = chosen per shape.
-int dkdv_blocks_override = 0;
-
+// key_blocks: 16-key blocks per wavefront of the dK/dV kernel, 0 = chosen per
+// shape; 1 or 2 force one kernel (kfm_fa_bwd_blocks, so tests reach both).
 template <typename T, int DP>
-int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
+int launch_bwd(const FaBwdParams& p, int key_blocks, hipStream_t stream) {
     const int64_t qblocks = (int64_t)p.n_qtiles * p.Hq * p.B;
     int64_t kblocks = (int64_t)p.n_ktiles * p.Hkv * p.B;
     // Two key blocks per wavefront (half the workgroups, each doing twice the
@@ -872,7 +870,7 @@ int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
     bool wide = false;
     if constexpr (DP <= 128) {
         const int64_t wblocks = ((int64_t)p.Nk + dkdv_wide_keys<DP>() - 1) / dkdv_wide_keys<DP>() * p.Hkv * p.B;
-        wide = dkdv_blocks_override ? dkdv_blocks_override == 2
+        wide = key_blocks ? key_blocks == 2
                                      : (!p.causal || DP > 32) && 2 * wblocks > device_cu_count();
         if (wide) kblocks = wblocks;
     }
@@ -902,12 +900,12 @@ int launch_bwd(const FaBwdParams& p, hipStream_t stream) {
 }
 
 template <typename T>
-int launch_bwd_dp(const FaBwdParams& p, int dp, hipStream_t stream) {
+int launch_bwd_dp(const FaBwdParams& p, int dp, int key_blocks, hipStream_t stream) {
     switch (dp) {
-        case 32: return launch_bwd<T, 32>(p, stream);
-        case 64: return launch_bwd<T, 64>(p, stream);
-        case 128: return launch_bwd<T, 128>(p, stream);
-        case 256: return launch_bwd<T, 256>(p, stream);
+        case 32: return launch_bwd<T, 32>(p, key_blocks, stream);
+        case 64: return launch_bwd<T, 64>(p, key_blocks, stream);
+        case 128: return launch_bwd<T, 128>(p, key_blocks, stream);
+        case 256: return launch_bwd<T, 256>(p, key_blocks, stream);
         default: set_error("fa_bwd: head dim %d not supported by this build", p.D); return KF_E_UNSUPPORTED;
     }
 }
@@ -921,27 +919,19 @@ bool bwd_dims_fit(int64_t B, int64_t Nq, int64_t Nk, int64_t Hq, int64_t Hkv, in
 }  // namespace
 }  // namespace kf
 
-// Measurement/test hook (not in the public header): force one (1) or two (2)
-// 16-key blocks per wavefront in the dK/dV kernel for head dims up to 128; 0
-// restores the per-shape choice.
-extern "C" int kfm_fa_bwd_key_blocks(int blocks) {
-    if (blocks < 0 || blocks > 2) return KF_E_INVALID;
-    kf::dkdv_blocks_override = blocks;
-    return KF_OK;
-}
-
 extern "C" int64_t kf_fa_bwd_workspace_bytes(int64_t B, int64_t Nq, int64_t Hq, int64_t D) {
     using namespace kf;
     if (B < 0 || Nq < 0 || Hq <= 0 || D <= 0 || D > 256 || !bwd_dims_fit(B, Nq, 0, Hq, 1, D)) return -1;
     return 2 * (int64_t)sizeof(float) * B * Hq * padded_rows(Nq, D);
 }
 
-extern "C" int kf_fa_bwd(const void* q, const void* k, const void* v, const void* o,
-                         const float* lse, const void* dout, void* dq, void* dk, void* dv,
-                         void* workspace, int64_t workspace_bytes, int64_t B, int64_t Nq,
-                         int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D, float scale, int causal,
-                         int dtype, kf_stream_t stream) {
-    using namespace kf;
+namespace kf {
+namespace {
+
+int fa_bwd_run(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+               void* dq, void* dk, void* dv, void* workspace, int64_t workspace_bytes, int64_t B, int64_t Nq,
+               int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D, float scale, int causal, int dtype, int key_blocks,
+               kf_stream_t stream) {
     KF_REQUIRE(bwd_dims_fit(B, Nq, Nk, Hq, Hkv, D), KF_E_INVALID, "fa_bwd: shape out of range");
     KF_REQUIRE(Hq > 0 && Hkv > 0 && Hq % Hkv == 0, KF_E_INVALID, "fa_bwd: Hq must be a positive multiple of Hkv");
     KF_REQUIRE(D > 0 && D % 8 == 0 && D <= 256, KF_E_INVALID,
@@ -972,5 +962,30 @@ extern "C" int kf_fa_bwd(const void* q, const void* k, const void* v, const void
     p.scale_log2 = scale * kLog2e;
     p.causal = causal ? 1 : 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    return dtype == KF_BF16 ? launch_bwd_dp<bf16>(p, dp, s) : launch_bwd_dp<f16>(p, dp, s);
+    return dtype == KF_BF16 ? launch_bwd_dp<bf16>(p, dp, key_blocks, s) : launch_bwd_dp<f16>(p, dp, key_blocks, s);
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int kf_fa_bwd(const void* q, const void* k, const void* v, const void* o,
+                         const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                         void* workspace, int64_t workspace_bytes, int64_t B, int64_t Nq,
+                         int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D, float scale, int causal,
+                         int dtype, kf_stream_t stream) {
+    return kf::fa_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, workspace, workspace_bytes, B, Nq, Nk, Hq, Hkv, D,
+                          scale, causal, dtype, 0, stream);
+}
+
+// Test entry point (not in the public header): kf_fa_bwd with the dK/dV
+// kernel's 16-key blocks per wavefront forced to one (1) or two (2) for head
+// dims up to 128; 0 keeps the per-shape choice.
+extern "C" int kfm_fa_bwd_blocks(const void* q, const void* k, const void* v, const void* o,
+                                 const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                                 void* workspace, int64_t workspace_bytes, int64_t B, int64_t Nq,
+                                 int64_t Nk, int64_t Hq, int64_t Hkv, int64_t D, float scale, int causal,
+                                 int dtype, int key_blocks, kf_stream_t stream) {
+    KF_REQUIRE(key_blocks >= 0 && key_blocks <= 2, KF_E_INVALID, "fa_bwd: key_blocks must be 0, 1 or 2");
+    return kf::fa_bwd_run(q, k, v, o, lse, dout, dq, dk, dv, workspace, workspace_bytes, B, Nq, Nk, Hq, Hkv, D,
+                          scale, causal, dtype, key_blocks, stream);
 }

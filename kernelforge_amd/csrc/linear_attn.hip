@@ -18,6 +18,7 @@
 // launches (split states, fixed-order split reduction, output).
 #include "kf_common.h"
 
+#include <atomic>
 #include <mutex>
 
 // Device scratch of kf_linattn_fwd_noalloc: the split partials and reduced
@@ -42,9 +43,6 @@ constexpr int KV_RING = 3;
 constexpr int Q_RING = 3;
 constexpr int kOutTokens = 64;      // tokens per output workgroup of the generic path
 constexpr int kSpinLimit = 1 << 20; // polls of the group counter before giving up
-// The limit the launches pass; only the test hook kfm_linattn_spin_limit
-// changes it, to drive the give-up path from the host.
-int g_spin_limit = kSpinLimit;
 
 // --------------------------------------------------------------------------
 // Control words at the start of the workspace (uint32):
@@ -227,8 +225,13 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
 // pair, sequence split), numbered by a ticket taken at start, so the members
 // of a group start consecutively: a member can only wait for members that
 // started before it or will start next, and at most one group is partly
-// started at any time (its waiting members hold fewer slots than one XCD
-// has), so every wait ends.
+// started at any time.  Workgroups of fully started groups wait for nobody
+// who has not started, so they finish and free their slots; the partly
+// started group's waiting members hold at most S - 1 slots, and the host
+// keeps S within the slots the device offers (invariant 3 below), so its
+// remaining members always find a slot and every wait ends.  Only other
+// work holding the device's slots for longer than the poll limit can make a
+// member give up (then it reports it: see group_barrier).
 //   Phase 1: stream the split's K and V (three 128-token tiles in flight in
 //            registers, LDS double buffer), accumulate the partial state
 //            S = V^T relu(K) with v_mfma_f32_32x32x16 and z = sum relu(K),
@@ -244,9 +247,28 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
 // ~19 us, phase 2 alone ~22 us, the two overlapping to ~33 us.  Phase 2 is
 // a mixed read/write stream of 128-byte spans; a probe of that traffic
 // alone reached ~4.2 TB/s at one 512-thread workgroup per CU.
+// OT (fp32 output only) writes out[b][h*D + r][t] -- LiteLA.attn_matmul's
+// [B, h, d, N] result -- instead of out[b][t][h*D + r].
+//
+// Memory-model invariants the group barrier and phase 2 rely on (any change
+// to either phase must keep them):
+//   1. Partials are written only with device-coherent (agent-scope) stores,
+//      and each writer waits for them (vmcnt(0)) before its workgroup
+//      barrier, which precedes its arrival count.
+//   2. Nothing reads a partial before the group barrier in a launch, and
+//      each (batch, head, split) partial starts on its own 128-byte line
+//      (kState floats are a whole number of lines), so no cache can hold a
+//      line of another group's or an earlier launch's partial: caches are
+//      invalidated at every kernel start.  Phase 2's plain loads therefore
+//      miss to the coherence point and see the stores of invariant 1.
+//   3. A group has at most as many members as can be resident at once
+//      (the host clamps the split count to the kernel's occupancy times the
+//      CU count), so the members a waiting workgroup needs can always start.
 // --------------------------------------------------------------------------
-template <typename T, typename TO>
+static_assert(kState * 4 % 128 == 0, "each partial starts on its own cache line");
+template <typename T, typename TO, bool OT = false>
 __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) {
+    static_assert(!OT || sizeof(TO) == 4, "the transposed output is fp32");
     constexpr int KV_BYTES = 2 * kTT * 256;                          // double-buffered K/V tile
     constexpr int Q_BYTES = kTT * 128;
     constexpr int O_BYTES = kTT * OutTile<TO>::ROW;
@@ -538,6 +560,26 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
     };
     auto out_store = [&](int i, int t0) {
         const unsigned char* ob = obuf(i);
+        if constexpr (OT) {
+            // Channel rows of out[b][c][t]: thread (tid % 128) owns token
+            // t0 + tid % 128 and channels (tid / 128) + 4k, so each store
+            // instruction of a wave writes 64 consecutive tokens (256 bytes)
+            // of one channel.
+            const int tok = tid & (kTT - 1), cq = tid >> 7;
+            if (t0 + tok < t_end) {
+                float* dst = reinterpret_cast<float*>(out) + ((int64_t)b * C + (int64_t)h0 * kD) * N + t0 + tok;
+#pragma unroll
+                for (int k = 0; k < 2 * kD / 4; ++k) {
+                    const int ch = cq + 4 * k;
+                    if (ch < nh * kD) {
+                        const float v = *reinterpret_cast<const float*>(ob + OutTile<TO>::off(tok, ch >> 2) +
+                                                                        (ch & 3) * 4);
+                        __builtin_nontemporal_store(v, dst + (int64_t)ch * N);
+                    }
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < OROUNDS; ++k) {
             const int c = k * kThreads + tid;
@@ -679,7 +721,7 @@ template <typename T, typename TO, int DG>
 __global__ __launch_bounds__(256) void linattn_out_generic(const T* __restrict__ qkv,
                                                            const float* __restrict__ state,
                                                            TO* __restrict__ out, int N, int H,
-                                                           float eps) {
+                                                           float eps, int out_tn) {
     constexpr int SS = (DG + 1) * DG;
     constexpr int TPI = 256 / DG > 0 ? 256 / DG : 1;  // tokens per pass (one thread per (t, r))
     const int h = blockIdx.x, b = blockIdx.z;
@@ -709,12 +751,16 @@ __global__ __launch_bounds__(256) void linattn_out_generic(const T* __restrict__
                     num = fmaf(st[r * DG + c], qt[tok][c], num);
                     den = fmaf(st[DG * DG + c], qt[tok][c], den);
                 }
-                out[((int64_t)b * N + t) * C + (int64_t)h * DG + r] = from_f32<TO>(num / (den + eps));
+                // out[b][t][c], or out[b][c][t] (LiteLA.attn_matmul's [B, h, d, N]) when out_tn.
+                const int64_t c_out = (int64_t)h * DG + r;
+                const int64_t o = out_tn ? ((int64_t)b * C + c_out) * N + t : ((int64_t)b * N + t) * C + c_out;
+                out[o] = from_f32<TO>(num / (den + eps));
             }
         }
     }
     }
 }
+
 
 // --------------------------------------------------------------------------
 // Host side.
@@ -730,6 +776,19 @@ int64_t split_len_for(int64_t N, int64_t splits, int64_t align) {
     return (len + align - 1) / align * align;
 }
 
+// Split plan of a request: `splits` (>= 1 after the default is applied) is
+// cut to the sequence length and to `max_members` (the fused kernel's
+// resident-workgroup capacity, or the generic path's grid limit), then each
+// split gets a whole number of `align`-token tiles; `eff` is the number of
+// non-empty splits that gives, never more than the cut request.
+void split_plan(int64_t N, int64_t splits, int64_t align, int64_t max_members, int64_t* len, int64_t* eff) {
+    if (splits > N) splits = N;
+    if (splits > max_members) splits = max_members;
+    if (splits < 1) splits = 1;
+    *len = split_len_for(N, splits, align);
+    *eff = (N + *len - 1) / *len;
+}
+
 // Workspace regions: control words, split partials, reduced states (the
 // generic path's; the fused kernel keeps its state in registers).
 struct Workspace {
@@ -738,84 +797,286 @@ struct Workspace {
     float* state;
 };
 
-template <typename T, typename TO>
-int run_mfma(const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
-             int split_len, float eps, hipStream_t stream) {
+// One resolved call.
+struct Launch {
+    const void* qkv;
+    void* out;
+    Workspace ws;
+    int B, N, H, D, S, L;  // S splits of L tokens
+    float eps;
+    int spin_limit;
+    bool out_tn;           // out[b][c][t] instead of out[b][t][c]
+    hipStream_t stream;
+};
+
+// Workgroups of one fused-kernel instantiation that the current device holds
+// at once: the occupancy per CU (LDS and registers decide it: one for fp32
+// output, whose phase-2 tiles take 96 KiB of LDS) times the CU count.
+template <typename T, typename TO, bool OT>
+int64_t fused_slots() {
+    static std::atomic<int> per_cu[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = per_cu[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, linattn_fused_kernel<T, TO, OT>, kThreads, 0) !=
+                hipSuccess ||
+            blocks < 1) {
+            (void)hipGetLastError();
+            blocks = 1;  // the query failed: assume the least
+        }
+        per_cu[dev].store(blocks, std::memory_order_relaxed);
+        n = blocks;
+    }
+    return (int64_t)n * device_cu_count();
+}
+
+int64_t fused_slots_for(int in_dt, int out_dt, bool ot) {
+    if (in_dt == KF_BF16) {
+        if (ot) return fused_slots<bf16, float, true>();
+        return out_dt == KF_F32 ? fused_slots<bf16, float, false>()
+               : out_dt == KF_F16 ? fused_slots<bf16, f16, false>() : fused_slots<bf16, bf16, false>();
+    }
+    if (ot) return fused_slots<f16, float, true>();
+    return out_dt == KF_F32 ? fused_slots<f16, float, false>()
+           : out_dt == KF_F16 ? fused_slots<f16, f16, false>() : fused_slots<f16, bf16, false>();
+}
+
+template <typename T, typename TO, bool OT>
+int run_mfma(const Launch& a) {
     FusedParams p;
-    p.qkv = qkv;
-    p.out = out;
-    p.partial = ws.partial;
-    p.ctrl = ws.ctrl;
-    p.N = N;
-    p.H = H;
-    p.npairs = (H + 1) / 2;
-    p.S = splits;
-    p.split_len = split_len;
-    p.spin_limit = g_spin_limit;
-    p.eps = eps;
-    const int64_t groups = (int64_t)B * p.npairs;
+    p.qkv = a.qkv;
+    p.out = a.out;
+    p.partial = a.ws.partial;
+    p.ctrl = a.ws.ctrl;
+    p.N = a.N;
+    p.H = a.H;
+    p.npairs = (a.H + 1) / 2;
+    p.S = a.S;
+    p.split_len = a.L;
+    p.spin_limit = a.spin_limit;
+    p.eps = a.eps;
+    const int64_t groups = (int64_t)a.B * p.npairs;
     // Groups per launch: the control region holds kMaxGroupsPerLaunch groups,
     // and a launch's workgroup count stays below 2^31.
     int64_t per = kMaxGroupsPerLaunch;
-    if (per * splits > 0x7fffffffLL) per = 0x7fffffffLL / splits;
+    if (per * a.S > 0x7fffffffLL) per = 0x7fffffffLL / a.S;
     for (int64_t g0 = 0; g0 < groups; g0 += per) {
         const int64_t n = groups - g0 < per ? groups - g0 : per;
         p.g0 = (int)g0;
-        p.total = (int)(n * splits);
-        hipLaunchKernelGGL((linattn_fused_kernel<T, TO>), dim3((unsigned)p.total), dim3(kThreads), 0, stream, p);
+        p.total = (int)(n * a.S);
+        hipLaunchKernelGGL((linattn_fused_kernel<T, TO, OT>), dim3((unsigned)p.total), dim3(kThreads), 0, a.stream,
+                           p);
         if (int rc = check_launch("linattn_fused_kernel launch")) return rc;
     }
     return KF_OK;
 }
 
 template <typename T, typename TO, int DG>
-int run_generic(const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
-                int split_len, float eps, hipStream_t stream) {
-    hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(H, splits, B), dim3(256), 0, stream,
-                       static_cast<const T*>(qkv), ws.partial, N, H, split_len, splits);
+int run_generic(const Launch& a) {
+    hipLaunchKernelGGL((linattn_state_generic<T, DG>), dim3(a.H, a.S, a.B), dim3(256), 0, a.stream,
+                       static_cast<const T*>(a.qkv), a.ws.partial, a.N, a.H, a.L, a.S);
     if (int rc = check_launch("linattn_state_generic launch")) return rc;
-    if (int rc = launch_reduce(ws.partial, ws.state, (int64_t)B * H, splits, (DG + 1) * DG, stream)) return rc;
-    hipLaunchKernelGGL((linattn_out_generic<T, TO, DG>),
-                       dim3(H, out_grid_y(N), B), dim3(256), 0, stream,
-                       static_cast<const T*>(qkv), ws.state, static_cast<TO*>(out), N, H, eps);
+    if (int rc = launch_reduce(a.ws.partial, a.ws.state, (int64_t)a.B * a.H, a.S, (DG + 1) * DG, a.stream))
+        return rc;
+    hipLaunchKernelGGL((linattn_out_generic<T, TO, DG>), dim3(a.H, out_grid_y(a.N), a.B), dim3(256), 0, a.stream,
+                       static_cast<const T*>(a.qkv), a.ws.state, static_cast<TO*>(a.out), a.N, a.H, a.eps,
+                       a.out_tn ? 1 : 0);
     return check_launch("linattn_out_generic launch");
 }
 
 template <typename T, typename TO>
-int run_generic_d(int D, const void* qkv, void* out, const Workspace& ws, int B, int N, int H, int splits,
-                  int split_len, float eps, hipStream_t stream) {
+int run_generic_d(const Launch& a) {
 #define KF_GENERIC_CASE(DD) \
-    case DD: return run_generic<T, TO, DD>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
-    switch (D) {
+    case DD: return run_generic<T, TO, DD>(a);
+    switch (a.D) {
         KF_GENERIC_CASE(1) KF_GENERIC_CASE(2) KF_GENERIC_CASE(4) KF_GENERIC_CASE(8)
         KF_GENERIC_CASE(16) KF_GENERIC_CASE(32) KF_GENERIC_CASE(64) KF_GENERIC_CASE(128)
-        default: set_error("linattn: unsupported head dim %d", D); return KF_E_UNSUPPORTED;
+        default: set_error("linattn: unsupported head dim %d", a.D); return KF_E_UNSUPPORTED;
     }
 #undef KF_GENERIC_CASE
 }
 
 template <typename T>
-int run_in(int out_dt, bool mfma, int D, const void* qkv, void* out, const Workspace& ws, int B, int N,
-           int H, int splits, int split_len, float eps, hipStream_t stream) {
+int run_in(int out_dt, bool mfma, const Launch& a) {
     if (mfma) {
         if constexpr (sizeof(T) == 2) {
+            if (a.out_tn) return run_mfma<T, float, true>(a);  // fp32 output only (checked by the caller)
             switch (out_dt) {
-                case KF_F32: return run_mfma<T, float>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
-                case KF_F16: return run_mfma<T, f16>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
-                case KF_BF16: return run_mfma<T, bf16>(qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+                case KF_F32: return run_mfma<T, float, false>(a);
+                case KF_F16: return run_mfma<T, f16, false>(a);
+                case KF_BF16: return run_mfma<T, bf16, false>(a);
             }
         }
     }
     switch (out_dt) {
-        case KF_F32: return run_generic_d<T, float>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
-        case KF_F16: return run_generic_d<T, f16>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
-        case KF_BF16: return run_generic_d<T, bf16>(D, qkv, out, ws, B, N, H, splits, split_len, eps, stream);
+        case KF_F32: return run_generic_d<T, float>(a);
+        case KF_F16: return run_generic_d<T, f16>(a);
+        case KF_BF16: return run_generic_d<T, bf16>(a);
     }
     set_error("linattn: unknown output dtype %d", out_dt);
     return KF_E_INVALID;
 }
 
 bool valid_dim(int64_t D) { return D > 0 && D <= 128 && 128 % D == 0; }
+
+// Argument checks shared by every entry point, before any device call.
+int validate(int64_t batch, int64_t seq_len, int64_t heads, int64_t dim, int in_dtype, int out_dtype) {
+    KF_REQUIRE(batch >= 0 && seq_len >= 0 && heads >= 0, KF_E_INVALID,
+               "linattn: negative shape B=%lld N=%lld H=%lld", (long long)batch,
+               (long long)seq_len, (long long)heads);
+    KF_REQUIRE(valid_dim(dim), KF_E_INVALID, "linattn: dim must divide 128 and be at most 128, got %lld",
+               (long long)dim);
+    KF_REQUIRE(in_dtype == KF_F32 || in_dtype == KF_F16 || in_dtype == KF_BF16, KF_E_INVALID,
+               "linattn: unknown input dtype %d", in_dtype);
+    KF_REQUIRE(out_dtype == KF_F32 || out_dtype == KF_F16 || out_dtype == KF_BF16, KF_E_INVALID,
+               "linattn: unknown output dtype %d", out_dtype);
+    KF_REQUIRE(batch <= 65535 && heads <= 65535 && seq_len <= 0x3fffffff, KF_E_UNSUPPORTED,
+               "linattn: shape exceeds grid limits");
+    return KF_OK;
+}
+
+// The fused kernel is the candidate for head dim 32 and 16-bit input (it also
+// needs 16-byte aligned buffers, which only the run itself can check).
+bool fused_candidate(int64_t dim, int in_dtype) { return dim == kD && in_dtype != KF_F32; }
+
+// Effective split count of a validated, non-empty request: the default for
+// splits <= 0, then the split plan, with the fused kernel's group size kept
+// within the workgroups the device holds at once (invariant 3 of the fused
+// kernel); `len` receives the split length.
+int64_t resolve_splits(int64_t batch, int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, int in_dtype,
+                       int out_dtype, bool out_tn, int64_t* len) {
+    if (splits <= 0) splits = kf_linattn_default_splits(batch, heads, dim, seq_len);
+    const bool fused = fused_candidate(dim, in_dtype) && (!out_tn || out_dtype == KF_F32);
+    int64_t max_members = 65535;  // the generic path's split index is a y grid dimension
+    if (fused) {
+        const int64_t slots = fused_slots_for(in_dtype, out_dtype, out_tn);
+        if (slots < max_members) max_members = slots;
+    }
+    int64_t eff = 1;
+    split_plan(seq_len, splits, fused ? kTT : kGT, max_members, len, &eff);
+    return eff;
+}
+
+// Zeroes the first `bytes` of a workspace (rounded down to whole words).
+int zero_words(void* ws, int64_t bytes, hipStream_t s) {
+    const int64_t n = bytes / 4;
+    if (n <= 0) return KF_OK;
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(linattn_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<unsigned*>(ws), n);
+    return check_launch("linattn_zero_kernel launch");
+}
+
+// Runs a validated, non-empty request with `workspace` holding the control
+// words, the partials and (generic path) the reduced states.
+int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_bytes, int64_t batch,
+                int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
+                int out_dtype, bool out_tn, int spin_limit, hipStream_t s) {
+    KF_REQUIRE(qkv && out, KF_E_INVALID, "linattn: null pointer");
+    int64_t split_len = 0;
+    const int64_t eff = resolve_splits(batch, seq_len, heads, dim, splits, in_dtype, out_dtype, out_tn, &split_len);
+    const int64_t need = kf_linattn_workspace_bytes(batch, heads, dim, eff);
+    KF_REQUIRE(workspace && workspace_bytes >= need, KF_E_WORKSPACE,
+               "linattn: workspace of %lld bytes needed, %lld given", (long long)need,
+               (long long)workspace_bytes);
+    KF_REQUIRE((uintptr_t)workspace % 256 == 0, KF_E_WORKSPACE, "linattn: workspace must be 256-byte aligned");
+    const bool mfma = fused_candidate(dim, in_dtype) && (!out_tn || out_dtype == KF_F32) &&
+                      (uintptr_t)qkv % 16 == 0 && (uintptr_t)out % 16 == 0;
+    if (!mfma && fused_candidate(dim, in_dtype)) {
+        // Unaligned buffers (or 16-bit transposed output): the generic path,
+        // with its own tile alignment and at most `eff` splits.
+        int64_t eff_generic = 0;
+        split_plan(seq_len, eff, kGT, 65535, &split_len, &eff_generic);
+    }
+    Launch a;
+    a.qkv = qkv;
+    a.out = out;
+    a.ws.ctrl = static_cast<unsigned*>(workspace);
+    a.ws.partial = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kCtrlBytes);
+    a.B = (int)batch;
+    a.N = (int)seq_len;
+    a.H = (int)heads;
+    a.D = (int)dim;
+    a.L = (int)split_len;
+    a.S = (int)((seq_len + split_len - 1) / split_len);  // <= eff
+    a.ws.state = a.ws.partial + batch * heads * (dim + 1) * dim * a.S;
+    a.eps = eps;
+    a.spin_limit = spin_limit;
+    a.out_tn = out_tn;
+    a.stream = s;
+    switch (in_dtype) {
+        case KF_BF16: return run_in<bf16>(out_dtype, mfma, a);
+        case KF_F16: return run_in<f16>(out_dtype, mfma, a);
+        default: return run_in<float>(out_dtype, false, a);
+    }
+}
+
+// Per-device address of `scratch`, resolved once per device with that
+// device current (each GPU holds its own copy at its own address).  The
+// first call on a device also zeroes the scratch's control words on the
+// caller's stream (the array starts zeroed at load; this makes it explicit).
+int scratch_for_current_device(void** ptr, hipStream_t stream) {
+    static std::mutex lock;
+    static void* addr[64] = {};
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return hip_failure(err, "linattn: hipGetDevice");
+    KF_REQUIRE(dev >= 0 && dev < 64, KF_E_UNSUPPORTED, "linattn: device ordinal %d out of range", dev);
+    std::lock_guard<std::mutex> guard(lock);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return hip_failure(err, "linattn: hipGetSymbolAddress(scratch)");
+        if (int rc = zero_words(p, kCtrlBytes, stream)) return rc;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return KF_OK;
+}
+
+// Reads the error word of a control region after `stream` has drained; when
+// it is set, clears the whole control region (a ticket counter may be left
+// over too) and reports what happened.
+int check_ctrl(unsigned* ctrl, hipStream_t stream) {
+    unsigned word = 0;
+    hipError_t err = hipMemcpyAsync(&word, ctrl + 1, sizeof(word), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return hip_failure(err, "linattn check: reading the error word");
+    if (word == 0) return KF_OK;
+    if (int rc = zero_words(ctrl, kCtrlBytes, stream)) return rc;
+    err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) return hip_failure(err, "linattn check: clearing the control words");
+    if (word == 1)
+        set_error("linattn: split workgroups of a (batch, head pair) stopped waiting for the rest of their "
+                  "group (other work held the device's slots past the poll limit); their outputs are NaN");
+    else
+        set_error("linattn: the workspace's control words were not zero on entry (error word %u); "
+                  "outputs are incomplete", word);
+    return KF_E_INCOMPLETE;
+}
+
+// Validates, then runs kf_linattn_fwd's request on the static scratch.
+int noalloc_run(const void* qkv, void* out, int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
+                int64_t splits, float eps, int in_dtype, int out_dtype, hipStream_t s) {
+    if (int rc = validate(batch, seq_len, heads, dim, in_dtype, out_dtype)) return rc;
+    if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
+    // Size check before any device work.
+    int64_t len = 0;
+    const int64_t eff = resolve_splits(batch, seq_len, heads, dim, splits, in_dtype, out_dtype, false, &len);
+    const int64_t need = kf_linattn_workspace_bytes(batch, heads, dim, eff);
+    KF_REQUIRE(need <= kLinattnScratchBytes, KF_E_WORKSPACE,
+               "linattn noalloc: %lld bytes of scratch needed for B=%lld H=%lld D=%lld splits=%lld, "
+               "the static scratch holds %lld; use fewer splits or kf_linattn_fwd with a workspace",
+               (long long)need, (long long)batch, (long long)heads, (long long)dim, (long long)eff,
+               (long long)kLinattnScratchBytes);
+    KF_REQUIRE(qkv && out, KF_E_INVALID, "linattn: null pointer");
+    void* ws = nullptr;
+    if (int rc = scratch_for_current_device(&ws, s)) return rc;
+    return linattn_run(qkv, out, ws, kLinattnScratchBytes, batch, seq_len, heads, dim, eff, eps, in_dtype,
+                       out_dtype, false, kSpinLimit, s);
+}
 
 }  // namespace
 }  // namespace kf
@@ -853,91 +1114,6 @@ extern "C" int64_t kf_linattn_workspace_bytes(int64_t batch, int64_t heads, int6
     return kf::kCtrlBytes + (int64_t)sizeof(float) * batch * heads * state * (splits + 1);
 }
 
-namespace kf {
-namespace {
-
-// Zeroes the first `bytes` of a workspace (rounded down to whole words).
-int zero_words(void* ws, int64_t bytes, hipStream_t s) {
-    const int64_t n = bytes / 4;
-    if (n <= 0) return KF_OK;
-    int64_t blocks = (n + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(linattn_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<unsigned*>(ws), n);
-    return check_launch("linattn_zero_kernel launch");
-}
-
-// Validates the request, resolves the split count and runs the kernels with
-// `workspace` holding the control words, the partials and (generic path)
-// the reduced states.
-int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_bytes, int64_t batch,
-                int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
-                int out_dtype, hipStream_t s) {
-    KF_REQUIRE(batch >= 0 && seq_len >= 0 && heads >= 0, KF_E_INVALID,
-               "linattn: negative shape B=%lld N=%lld H=%lld", (long long)batch,
-               (long long)seq_len, (long long)heads);
-    KF_REQUIRE(valid_dim(dim), KF_E_INVALID, "linattn: dim must divide 128 and be at most 128, got %lld",
-               (long long)dim);
-    KF_REQUIRE(in_dtype == KF_F32 || in_dtype == KF_F16 || in_dtype == KF_BF16, KF_E_INVALID,
-               "linattn: unknown input dtype %d", in_dtype);
-    KF_REQUIRE(out_dtype == KF_F32 || out_dtype == KF_F16 || out_dtype == KF_BF16, KF_E_INVALID,
-               "linattn: unknown output dtype %d", out_dtype);
-    if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
-    KF_REQUIRE(qkv && out, KF_E_INVALID, "linattn: null pointer");
-    KF_REQUIRE(batch <= 65535 && heads <= 65535 && seq_len <= 0x3fffffff, KF_E_UNSUPPORTED,
-               "linattn: shape exceeds grid limits");
-    if (splits <= 0) splits = kf_linattn_default_splits(batch, heads, dim, seq_len);
-    if (splits > seq_len) splits = seq_len;
-    const int64_t need = kf_linattn_workspace_bytes(batch, heads, dim, splits);
-    KF_REQUIRE(workspace && workspace_bytes >= need, KF_E_WORKSPACE,
-               "linattn: workspace of %lld bytes needed, %lld given", (long long)need,
-               (long long)workspace_bytes);
-    KF_REQUIRE((uintptr_t)workspace % 256 == 0, KF_E_WORKSPACE, "linattn: workspace must be 256-byte aligned");
-    const bool mfma = dim == kD && in_dtype != KF_F32 && (uintptr_t)qkv % 16 == 0 &&
-                      (uintptr_t)out % 16 == 0;
-    // The generic path's split index is a y grid dimension (at most 65535).
-    const int64_t split_len = split_len_for(seq_len, splits < 65535 ? splits : 65535, mfma ? kTT : kGT);
-    const int64_t eff_splits = (seq_len + split_len - 1) / split_len;
-    KF_REQUIRE(eff_splits <= 65535, KF_E_UNSUPPORTED, "linattn: too many splits");
-    const int64_t state_size = (dim + 1) * dim;
-    Workspace ws;
-    ws.ctrl = static_cast<unsigned*>(workspace);
-    ws.partial = reinterpret_cast<float*>(static_cast<unsigned char*>(workspace) + kCtrlBytes);
-    ws.state = ws.partial + batch * heads * state_size * splits;
-    const int B = (int)batch, N = (int)seq_len, H = (int)heads, D = (int)dim;
-    const int S = (int)eff_splits, L = (int)split_len;
-    switch (in_dtype) {
-        case KF_BF16: return run_in<bf16>(out_dtype, mfma, D, qkv, out, ws, B, N, H, S, L, eps, s);
-        case KF_F16: return run_in<f16>(out_dtype, mfma, D, qkv, out, ws, B, N, H, S, L, eps, s);
-        default: return run_in<float>(out_dtype, false, D, qkv, out, ws, B, N, H, S, L, eps, s);
-    }
-}
-
-// Per-device address of `scratch`, resolved once per device with that
-// device current (each GPU holds its own copy at its own address).  The
-// first call on a device also zeroes the scratch's control words on the
-// caller's stream (the array starts zeroed at load; this makes it explicit).
-int scratch_for_current_device(void** ptr, hipStream_t stream) {
-    static std::mutex lock;
-    static void* addr[64] = {};
-    int dev = 0;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return hip_failure(err, "linattn: hipGetDevice");
-    KF_REQUIRE(dev >= 0 && dev < 64, KF_E_UNSUPPORTED, "linattn: device ordinal %d out of range", dev);
-    std::lock_guard<std::mutex> guard(lock);
-    if (!addr[dev]) {
-        void* p = nullptr;
-        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (err != hipSuccess) return hip_failure(err, "linattn: hipGetSymbolAddress(scratch)");
-        if (int rc = zero_words(p, kCtrlBytes, stream)) return rc;
-        addr[dev] = p;
-    }
-    *ptr = addr[dev];
-    return KF_OK;
-}
-
-}  // namespace
-}  // namespace kf
-
 extern "C" int kf_linattn_workspace_init(void* workspace, int64_t workspace_bytes, kf_stream_t stream) {
     using namespace kf;
     KF_REQUIRE(workspace_bytes >= 0, KF_E_INVALID, "linattn: negative workspace size");
@@ -950,38 +1126,68 @@ extern "C" int kf_linattn_fwd(const void* qkv, void* out, void* workspace, int64
                               int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
                               int64_t splits, float eps, int in_dtype, int out_dtype,
                               kf_stream_t stream) {
-    return kf::linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps,
-                           in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+    using namespace kf;
+    if (int rc = validate(batch, seq_len, heads, dim, in_dtype, out_dtype)) return rc;
+    if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
+    return linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps, in_dtype,
+                       out_dtype, false, kSpinLimit, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kf_linattn_attn_matmul(const void* qkv, float* out, void* workspace, int64_t workspace_bytes,
+                                      int64_t batch, int64_t seq_len, int64_t heads, int64_t dim,
+                                      int64_t splits, float eps, int in_dtype, kf_stream_t stream) {
+    using namespace kf;
+    if (int rc = validate(batch, seq_len, heads, dim, in_dtype, KF_F32)) return rc;
+    if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
+    return linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps, in_dtype,
+                       KF_F32, true, kSpinLimit, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kf_linattn_check(void* workspace, int64_t workspace_bytes, kf_stream_t stream) {
+    using namespace kf;
+    KF_REQUIRE(workspace && workspace_bytes >= kCtrlBytes, KF_E_WORKSPACE,
+               "linattn check: a workspace of at least %lld bytes is needed", (long long)kCtrlBytes);
+    return check_ctrl(static_cast<unsigned*>(workspace), static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t kf_linattn_noalloc_max_bytes(void) { return kLinattnScratchBytes; }
 
-// Test hook, not part of the public ABI: sets the polls a member of the fused
-// kernel makes at its group's counter before giving up (and writing NaN);
-// polls <= 0 restores the default.  Not thread-safe; tests only.
-extern "C" int kfm_linattn_spin_limit(int64_t polls) {
-    kf::g_spin_limit = polls <= 0 ? kf::kSpinLimit : (int)(polls < kf::kSpinLimit ? polls : kf::kSpinLimit);
-    return KF_OK;
-}
-
 extern "C" int kf_linattn_fwd_noalloc(const void* qkv, void* out, int64_t batch, int64_t seq_len,
                                       int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
                                       int out_dtype, kf_stream_t stream) {
-    using namespace kf;
-    // Size check first, so an oversized request fails before any device call.
-    int64_t eff = splits <= 0 ? kf_linattn_default_splits(batch, heads, dim, seq_len) : splits;
-    if (eff > seq_len && seq_len > 0) eff = seq_len;
-    const int64_t need = kf_linattn_workspace_bytes(batch, heads, dim, eff);
-    KF_REQUIRE(need <= kLinattnScratchBytes, KF_E_WORKSPACE,
-               "linattn noalloc: %lld bytes of scratch needed for B=%lld H=%lld D=%lld splits=%lld, "
-               "the static scratch holds %lld; use fewer splits or kf_linattn_fwd with a workspace",
-               (long long)need, (long long)batch, (long long)heads, (long long)dim, (long long)eff,
-               (long long)kLinattnScratchBytes);
-    if (batch <= 0 || seq_len <= 0 || heads <= 0)
-        return linattn_run(qkv, out, nullptr, 0, batch, seq_len, heads, dim, eff, eps, in_dtype, out_dtype,
+    return kf::noalloc_run(qkv, out, batch, seq_len, heads, dim, splits, eps, in_dtype, out_dtype,
                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int kf_linattn_noalloc_check(kf_stream_t stream) {
+    using namespace kf;
     void* ws = nullptr;
     if (int rc = scratch_for_current_device(&ws, static_cast<hipStream_t>(stream))) return rc;
-    return linattn_run(qkv, out, ws, kLinattnScratchBytes, batch, seq_len, heads, dim, eff, eps, in_dtype,
-                       out_dtype, static_cast<hipStream_t>(stream));
+    return check_ctrl(static_cast<unsigned*>(ws), static_cast<hipStream_t>(stream));
+}
+
+// Test entry points (not in the public header).
+//
+// kf_linattn_fwd with the number of polls a member of the fused kernel makes
+// at its group's counter before giving up (and writing NaN); polls <= 0 or
+// above the default take the default.  Lets a test drive the give-up path
+// from the host without any global state.
+extern "C" int kfm_linattn_fwd_spin(const void* qkv, void* out, void* workspace, int64_t workspace_bytes,
+                                    int64_t batch, int64_t seq_len, int64_t heads, int64_t dim, int64_t splits,
+                                    float eps, int in_dtype, int out_dtype, int64_t polls, kf_stream_t stream) {
+    using namespace kf;
+    if (int rc = validate(batch, seq_len, heads, dim, in_dtype, out_dtype)) return rc;
+    if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
+    const int spin = polls <= 0 || polls > kSpinLimit ? kSpinLimit : (int)polls;
+    return linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps, in_dtype,
+                       out_dtype, false, spin, static_cast<hipStream_t>(stream));
+}
+
+// The split plan's arithmetic (no device call): plan[0] = split length,
+// plan[1] = effective split count.
+extern "C" int kfm_linattn_split_plan(int64_t seq_len, int64_t splits, int64_t align, int64_t max_members,
+                                      int64_t* plan) {
+    if (seq_len <= 0 || align <= 0 || max_members <= 0 || !plan) return KF_E_INVALID;
+    kf::split_plan(seq_len, splits, align, max_members, &plan[0], &plan[1]);
+    return KF_OK;
 }

@@ -363,10 +363,6 @@ void litela_q_out_kernel(FusedLaParams p) {
 
 bool aligned_to(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
-// Heads per workgroup forced by kfm_litela_fused_heads (tests reach both
-// tile shapes with it); 0 = chosen per shape.
-int fused_heads_override = 0;
-
 template <typename T, int HG> int run_fused(FusedLaParams p, hipStream_t st) {
     p.HG = (p.H + HG - 1) / HG;
     const int grid = p.B * p.TT * p.HG;
@@ -397,14 +393,6 @@ int pick_heads_per_group(int B, int TT, int H) {
 }  // namespace
 }  // namespace kf
 
-// Measurement/test hook (not in the public header): force 3 or 4 heads per
-// workgroup, 0 restores the per-shape choice.
-extern "C" int kfm_litela_fused_heads(int heads_per_group) {
-    if (heads_per_group != 0 && heads_per_group != 3 && heads_per_group != 4) return KF_E_INVALID;
-    kf::fused_heads_override = heads_per_group;
-    return KF_OK;
-}
-
 extern "C" int64_t kf_litela_fused_workspace_bytes(int64_t batch, int64_t seq_len, int64_t heads) {
     using namespace kf;
     if (batch < 0 || seq_len < 0 || heads < 1) return -1;
@@ -412,10 +400,13 @@ extern "C" int64_t kf_litela_fused_workspace_bytes(int64_t batch, int64_t seq_le
     return 4 * batch * heads * kHState * (tt + 1);
 }
 
-extern "C" int kf_litela_fused_attn(const void* x, const void* qkv_weight, const void* qkv_bias, void* out,
-                                    void* workspace, int64_t workspace_bytes, int64_t batch, int64_t seq_len,
-                                    int64_t heads, int64_t dim, float eps, int dtype, kf_stream_t stream) {
-    using namespace kf;
+namespace kf {
+namespace {
+
+// heads_per_group: 3 or 4 heads per workgroup, 0 = chosen per shape.
+int litela_fused_run(const void* x, const void* qkv_weight, const void* qkv_bias, void* out, void* workspace,
+                     int64_t workspace_bytes, int64_t batch, int64_t seq_len, int64_t heads, int64_t dim, float eps,
+                     int dtype, int heads_per_group, kf_stream_t stream) {
     clear_error();
     KF_REQUIRE(dtype == KF_BF16 || dtype == KF_F16, KF_E_INVALID, "kf_litela_fused_attn: dtype must be bf16 or f16");
     KF_REQUIRE(dim == kHD, KF_E_UNSUPPORTED, "kf_litela_fused_attn: head dim must be 32, got %lld", (long long)dim);
@@ -450,7 +441,30 @@ extern "C" int kf_litela_fused_attn(const void* x, const void* qkv_weight, const
     p.TT = (int)tt;
     p.eps = eps;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int hg = fused_heads_override > 0 ? fused_heads_override : pick_heads_per_group(p.B, p.TT, p.H);
+    const int hg = heads_per_group > 0 ? heads_per_group : pick_heads_per_group(p.B, p.TT, p.H);
     if (hg == 3) return dtype == KF_BF16 ? run_fused<bf16, 3>(p, st) : run_fused<f16, 3>(p, st);
     return dtype == KF_BF16 ? run_fused<bf16, 4>(p, st) : run_fused<f16, 4>(p, st);
+}
+
+}  // namespace
+}  // namespace kf
+
+extern "C" int kf_litela_fused_attn(const void* x, const void* qkv_weight, const void* qkv_bias, void* out,
+                                    void* workspace, int64_t workspace_bytes, int64_t batch, int64_t seq_len,
+                                    int64_t heads, int64_t dim, float eps, int dtype, kf_stream_t stream) {
+    return kf::litela_fused_run(x, qkv_weight, qkv_bias, out, workspace, workspace_bytes, batch, seq_len, heads,
+                                dim, eps, dtype, 0, stream);
+}
+
+// Test entry point (not in the public header): kf_litela_fused_attn with 3 or
+// 4 heads per workgroup forced (0 keeps the per-shape choice), so tests reach
+// both tile shapes.
+extern "C" int kfm_litela_fused_attn_heads(const void* x, const void* qkv_weight, const void* qkv_bias, void* out,
+                                           void* workspace, int64_t workspace_bytes, int64_t batch, int64_t seq_len,
+                                           int64_t heads, int64_t dim, float eps, int dtype, int heads_per_group,
+                                           kf_stream_t stream) {
+    KF_REQUIRE(heads_per_group == 0 || heads_per_group == 3 || heads_per_group == 4, KF_E_INVALID,
+               "kf_litela_fused_attn: heads per workgroup must be 0, 3 or 4");
+    return kf::litela_fused_run(x, qkv_weight, qkv_bias, out, workspace, workspace_bytes, batch, seq_len, heads,
+                                dim, eps, dtype, heads_per_group, stream);
 }

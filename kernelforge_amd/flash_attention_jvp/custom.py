@@ -93,6 +93,14 @@ def _dims(q, k):
     return q.shape[0], q.shape[1], k.shape[1], q.shape[2], k.shape[2], q.shape[3]
 
 
+def _check_cached(q, out, lse):
+    """The cached forward results: out like q, LSE fp32 [B, Hq, Nq] (custom.py:204-207)."""
+    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+        raise ValueError("out must have q's shape, device, and dtype")
+    if lse.shape != (q.shape[0], q.shape[2], q.shape[1]) or lse.dtype != torch.float32 or lse.device != q.device:
+        raise ValueError("lse must be float32 [B, Hq, Nq] on q's device")
+
+
 # ---------------------------------------------------------------------------
 # Opaque operators (C ABI launches on the current stream).
 # ---------------------------------------------------------------------------
@@ -123,9 +131,15 @@ def _launch_jvp(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tq: torch.Ten
     arguments are accepted for schema compatibility; the kernel runs its own
     tile for the head dim.  A tangent with no elements stands for a zero
     tangent, whose products the kernel skips (the reference passes explicit
-    zeros, which give the same result)."""
+    zeros, which give the same result).  Every argument is checked here, so a
+    direct ``torch.ops.kernelforge.flash_attention_jvp`` call gets the same
+    ValueErrors as the Python wrapper, never an out-of-bounds launch."""
+    _validate_inputs(q, k, v, scale)
+    _check_cached(q, out, lse)
+    tq, tk, tv = (None if t.numel() == 0 else _prepare_tangent(t, p, n)
+                  for t, p, n in zip((tq, tk, tv), (q, k, v), ("tq", "tk", "tv")))
+    q, k, v, out, lse = (x.contiguous() for x in (q, k, v, out, lse))
     B, Nq, Nk, Hq, Hkv, D = _dims(q, k)
-    tq, tk, tv = (t if t.numel() else None for t in (tq, tk, tv))
     tout = torch.empty_like(out)
     rc = _lib.load().kf_fa_jvp(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(tq), _lib.ptr(tk),
                                _lib.ptr(tv), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(tout),
@@ -231,10 +245,7 @@ def flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, *, softmax_scale=None, ca
     ``torch.ops.kernelforge.flash_attention_jvp`` (the reference's schema).
     """
     scale = _validate_inputs(q, k, v, softmax_scale)
-    if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
-        raise ValueError("out must have q's shape, device, and dtype")
-    if lse.shape != (q.shape[0], q.shape[2], q.shape[1]) or lse.dtype != torch.float32 or lse.device != q.device:
-        raise ValueError("lse must be float32 [B, Hq, Nq] on q's device")
+    _check_cached(q, out, lse)
     sched = _schedule(q.shape[-1])
     for key, val in (("block_m", block_m), ("block_n", block_n), ("threads", threads), ("num_stages", num_stages)):
         if val is not None:

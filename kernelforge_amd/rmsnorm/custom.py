@@ -196,6 +196,18 @@ def rms_norm_module_forward(x: torch.Tensor, weight: torch.Tensor, eps: float = 
     return _RMSNormFunction.apply(x, weight, eps)
 
 
+_unit_weights: dict[tuple, torch.Tensor] = {}
+
+
+def _unit_weight(dim: int, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A cached weight of ones: y = dt(x * inv) * 1 rounds to x's dtype once."""
+    key = (dim, dtype, str(device))
+    w = _unit_weights.get(key)
+    if w is None:
+        w = _unit_weights[key] = torch.ones(dim, dtype=dtype, device=device)
+    return w
+
+
 class RMSNorm(torch.nn.Module):
     """``RMSNorm(dim, scale_factor=1.0, eps=1e-6)`` (rmsnorm/original.py:9-52) on the HIP kernels.
 
@@ -211,6 +223,11 @@ class RMSNorm(torch.nn.Module):
         super().__init__()
         self.eps = eps
         self.weight = torch.nn.Parameter(torch.ones(dim) * scale_factor)
+
+    def _norm(self, x: torch.Tensor) -> torch.Tensor:
+        """``x * rsqrt(mean(x^2, -1) + eps)`` in x's dtype (rmsnorm/original.py:27-38)
+        on the HIP kernel, computed in fp32 and rounded once; differentiable in x."""
+        return rms_norm_module_forward(x, _unit_weight(x.shape[-1], x.dtype, x.device), self.eps)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return rms_norm_module_forward(x, self.weight, self.eps)

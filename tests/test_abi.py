@@ -60,18 +60,61 @@ def test_measurement_entry_points_are_exported_outside_the_header(lib):
         assert name.startswith("kfm_") and hasattr(raw, name), name
         assert name not in decls
     KF_E_INVALID = 1
+    bwd_args = (None,) * 9 + (None, 0, 1, 4, 4, 2, 2, 64, 0.1, 0, _lib.KF_BF16)
     for bad in (-1, 3):
-        assert lib.kfm_fa_bwd_key_blocks(bad) == KF_E_INVALID
-    assert lib.kfm_fa_bwd_key_blocks(0) == 0  # the per-shape choice (the default)
+        assert lib.kfm_fa_bwd_blocks(*bwd_args, bad, None) == KF_E_INVALID
+    assert lib.kfm_litela_fused_attn_heads(None, None, None, None, None, 0, 1, 16, 2, 32, 1e-15, _lib.KF_BF16, 5,
+                                           None) == KF_E_INVALID
     assert lib.kfm_copy(None, None, 15, 1, None) == KF_E_INVALID
-    assert lib.kfm_coissue(None, None, 4, 1, 0, 0, 2, None) == KF_E_INVALID
-    assert lib.kfm_lds_rate(None, None, 1, 0, 1, 0, None) == KF_E_INVALID
+    # no test entry point keeps global state: the old setter hooks are gone
+    for gone in ("kfm_fa_bwd_key_blocks", "kfm_litela_fused_heads", "kfm_linattn_spin_limit", "kfm_coissue",
+                 "kfm_lds_rate"):
+        assert not hasattr(raw, gone), gone
+
+
+def test_probe_library_is_separate(lib):
+    """The issue-rate probes live in their own library, not in the product's."""
+    if not _lib.PROBES_PATH.exists():
+        pytest.skip("probe library not built")
+    probes = _lib.load_probes()
+    assert probes.kfm_coissue(None, None, 4, 1, 0, 0, 2, None) == 1
+    assert probes.kfm_lds_rate(None, None, 1, 0, 1, 0, None) == 1
+
+
+def split_plan(lib, n, splits, align, max_members):
+    plan = (ctypes.c_int64 * 2)()
+    assert lib.kfm_linattn_split_plan(n, splits, align, max_members, plan) == 0
+    return plan[0], plan[1]
+
+
+def test_linattn_split_plan_arithmetic(lib):
+    """The split plan behind kf_linattn_fwd: the request is cut to the
+    sequence length and to the fused kernel's resident capacity, then every
+    split takes whole tiles; the effective count never exceeds the cut
+    request, the splits cover the sequence, and none is empty."""
+    # the regression case: N = 40000, 400 requested, 256 resident workgroups
+    assert split_plan(lib, 40000, 400, 128, 256) == (256, 157)
+    # without the cut the 400 requests give 313 members, more than 256 slots
+    assert split_plan(lib, 40000, 400, 128, 1 << 20) == (128, 313)
+    assert split_plan(lib, 4096, 3, 128, 256) == (1408, 3)
+    assert split_plan(lib, 16384, 7, 128, 256) == (2432, 7)
+    assert split_plan(lib, 5, 64, 128, 256) == (128, 1)
+    assert split_plan(lib, 1000, 1, 32, 65535) == (1024, 1)
+    for n in (1, 127, 128, 129, 4096, 40000, 1 << 20):
+        for req in (1, 2, 3, 7, 64, 255, 256, 257, 400, 100000):
+            for cap in (1, 7, 256, 512):
+                length, eff = split_plan(lib, n, req, 128, cap)
+                assert length % 128 == 0 and length > 0
+                assert 1 <= eff <= min(req, cap, n)
+                assert (eff - 1) * length < n <= eff * length  # covered, last split non-empty
+    assert lib.kfm_linattn_split_plan(0, 1, 128, 1, (ctypes.c_int64 * 2)()) == 1
 
 
 def test_version_and_status_strings(lib):
     assert lib.kf_abi_version() == _lib.ABI_VERSION == 1
     assert lib.kf_status_string(0) == b"KF_OK"
     assert lib.kf_status_string(3) == b"KF_E_WORKSPACE"
+    assert lib.kf_status_string(5) == b"KF_E_INCOMPLETE"
     assert lib.kf_status_string(99) == b"KF_E_UNKNOWN"
 
 
@@ -86,6 +129,11 @@ def test_host_side_validation_needs_no_device(lib):
     assert lib.kf_linattn_fwd(null, null, null, 0, 1, 8, 2, 48, 1, 1e-15, _lib.KF_BF16, _lib.KF_F32, null) == 1
     assert b"dim" in lib.kf_last_error()
     assert lib.kf_linattn_fwd(null, null, null, 0, 0, 8, 2, 32, 1, 1e-15, _lib.KF_BF16, _lib.KF_F32, null) == 0
+    # the no-allocation entry point validates before it resolves its scratch
+    assert lib.kf_linattn_fwd_noalloc(null, null, 1, 8, 2, 48, 1, 1e-15, _lib.KF_BF16, _lib.KF_F32, null) == 1
+    assert b"dim" in lib.kf_last_error()
+    assert lib.kf_linattn_attn_matmul(null, null, null, 0, 1, 8, 2, 32, 1, 1e-15, 9, null) == 1
+    assert lib.kf_linattn_check(null, 0, null) == 3
     assert lib.kf_fa_fwd(null, null, null, null, null, 1, 4, 4, 2, 2, 12, 0.3, 0, _lib.KF_BF16, null) == 1
     assert b"multiple of 8" in lib.kf_last_error()
     assert lib.kf_fa_fwd(null, null, null, null, null, 1, 4, 4, 3, 2, 64, 0.3, 0, _lib.KF_BF16, null) == 1

@@ -239,6 +239,31 @@ def test_validation_messages():
             call()
 
 
+def test_registered_operator_validates_direct_calls():
+    """torch.ops.kernelforge.flash_attention_jvp called directly (bypassing the
+    Python wrapper) checks its arguments before any launch, with the same
+    messages; non-contiguous primals are copied, giving the wrapper's result."""
+    q, k, v, tq, tk, tv = seeded((1, 9, 13, 2, 2, 64, False, None), torch.float16)
+    out, lse = flash_attention(q, k, v, return_lse=True)
+    op = torch.ops.kernelforge.flash_attention_jvp
+    scale = 64 ** -0.5
+    bad_calls = {
+        "tq": lambda: op(q, k, v, tq[:, :-1], tk, tv, out, lse, scale, False, 64, 64, 128, 1),
+        "tv": lambda: op(q, k, v, tq, tk, tv.float(), out, lse, scale, False, 64, 64, 128, 1),
+        "out": lambda: op(q, k, v, tq, tk, tv, out[:, :-1], lse, scale, False, 64, 64, 128, 1),
+        "lse": lambda: op(q, k, v, tq, tk, tv, out, lse[:, :1], scale, False, 64, 64, 128, 1),
+        "must match": lambda: op(q, k[:, :-1], v, tq, tk, tv, out, lse, scale, False, 64, 64, 128, 1),
+        "positive": lambda: op(q, k, v, tq, tk, tv, out, lse, -1.0, False, 64, 64, 128, 1),
+    }
+    for fragment, call in bad_calls.items():
+        with pytest.raises(ValueError, match=fragment):
+            call()
+    expected = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse)
+    qt = q.transpose(1, 2).contiguous().transpose(1, 2)  # same values, non-contiguous
+    assert not qt.is_contiguous()
+    assert torch.equal(op(qt, k, v, tq, tk, tv, out, lse, scale, False, 64, 64, 128, 1), expected)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("causal", (False, True))
 @pytest.mark.parametrize("stages", (1, 2, 3))
@@ -311,28 +336,35 @@ def test_reference_operator_schema():
 def test_baseline_config_fused():
     """B=2, H=16, N=4096, D=128 bf16, scale 1/sqrt(D), non-causal.
 
-    O, LSE and tO of the fused kernel against dense fp32 torch.func.jvp
-    (north-star tolerance 2e-2 / 2e-2) on 8 of the 32 (batch, head) slices,
-    with the oracle computing in fp32 on the fp32 values of the bf16 inputs.
-    Over the whole output: agreement with the two-launch path, exact
-    linearity in the tangents, finiteness.
+    On every one of the 32 (batch, head) slices, against dense fp32
+    torch.func.jvp (north-star tolerance 2e-2 / 2e-2; the oracle computes in
+    fp32 on the fp32 values of the bf16 inputs): O, LSE and tO of the fused
+    kernel, O and LSE of the forward, and tO of the standalone
+    ``flash_attention_jvp`` (the reference's drop-in) from that forward's O
+    and LSE.  Over the whole output: exact linearity in the tangents,
+    finiteness.
     """
     case = (2, 4096, 4096, 16, 16, 128, False, None)
     q, k, v, tq, tk, tv = seeded(case, torch.bfloat16, seed=0)
     out, lse, tangent = flash_attention_fwd_jvp(q, k, v, tq, tk, tv)
-    for b, h in ((0, 0), (0, 3), (0, 9), (0, 14), (1, 1), (1, 7), (1, 12), (1, 15)):
-        head = lambda t: t[b:b + 1, :, h:h + 1].cpu().float()  # noqa: E731
-        ref_out, ref_tangent = orc.attention_jvp(*(head(t) for t in (q, k, v, tq, tk, tv)))
-        assert ref_out.dtype == torch.float32 and ref_tangent.dtype == torch.float32
-        torch.testing.assert_close(head(out), ref_out, atol=2e-2, rtol=2e-2)
-        torch.testing.assert_close(head(tangent), ref_tangent, atol=2e-2, rtol=2e-2)
-        ref_lse = orc.attention_lse(head(q), head(k))
-        torch.testing.assert_close(lse[b:b + 1, h:h + 1].cpu(), ref_lse, atol=2e-3, rtol=1e-4)
     out_fwd, lse_fwd = flash_attention(q, k, v, return_lse=True)
+    standalone = flash_attention_jvp(q, k, v, tq, tk, tv, out_fwd, lse_fwd)
+    host = [t.cpu().float() for t in (q, k, v, tq, tk, tv, out, tangent, out_fwd, standalone)]
+    lse_h, lse_fwd_h = lse.cpu(), lse_fwd.cpu()
+    for b in range(2):
+        for h in range(16):
+            print(f"baseline FA slice b={b} h={h}", flush=True)
+            qs, ks, vs, tqs, tks, tvs, o, t, o_fwd, t_sa = (x[b:b + 1, :, h:h + 1] for x in host)
+            ref_out, ref_tangent = orc.attention_jvp(qs, ks, vs, tqs, tks, tvs)
+            assert ref_out.dtype == torch.float32 and ref_tangent.dtype == torch.float32
+            ref_lse = orc.attention_lse(qs, ks)
+            for name, got, ref in (("fused O", o, ref_out), ("fused tO", t, ref_tangent),
+                                   ("forward O", o_fwd, ref_out), ("standalone tO", t_sa, ref_tangent)):
+                torch.testing.assert_close(got, ref, atol=2e-2, rtol=2e-2, msg=lambda m: f"{name} b={b} h={h}: {m}")
+            for got in (lse_h, lse_fwd_h):
+                torch.testing.assert_close(got[b:b + 1, h:h + 1], ref_lse, atol=2e-3, rtol=1e-4)
     torch.testing.assert_close(out.float(), out_fwd.float(), atol=1e-6, rtol=2 * torch.finfo(torch.bfloat16).eps)
     assert torch.equal(lse, lse_fwd)
-    two_launch = flash_attention_jvp(q, k, v, tq, tk, tv, out_fwd, lse_fwd)
-    torch.testing.assert_close(two_launch.float(), tangent.float(), atol=2e-2, rtol=2e-2)
     doubled = flash_attention_fwd_jvp(q, k, v, 2 * tq, 2 * tk, 2 * tv)[2]
     assert torch.equal(doubled, 2 * tangent)
     assert bool(torch.isfinite(tangent).all()) and bool(torch.isfinite(out).all())

@@ -92,33 +92,42 @@ def test_gradients_match_fp64(case, dtype):
         torch.testing.assert_close(actual.cpu().double(), ref, **tolerance(dtype), msg=lambda m: f"{name}: {m}")
 
 
-@pytest.fixture
-def key_blocks():
-    """Sets the dK/dV kernel's 16-key blocks per wavefront through the
-    library's test hook (1 or 2; head dims up to 128) and restores the
-    per-shape choice afterwards."""
+def bwd_blocks(dout, q, k, v, out, lse, blocks, causal=False, softmax_scale=None):
+    """The backward launch with the dK/dV kernel's 16-key blocks per wavefront
+    forced (1 or 2; head dims up to 128) through the library's per-call test
+    entry point kfm_fa_bwd_blocks; otherwise as flash_attention_backward."""
+    B, Nq, Hq, D = q.shape
+    Nk, Hkv = k.shape[1], k.shape[2]
+    scale = D ** -0.5 if softmax_scale is None else softmax_scale
     lib = _lib.load()
+    dq, dk, dv = (torch.empty_like(x, memory_format=torch.contiguous_format) for x in (q, k, v))
+    ws_bytes = lib.kf_fa_bwd_workspace_bytes(B, Nq, Hq, D)
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    q, k, v, dout, out, lse = (x.contiguous() for x in (q, k, v, dout, out, lse))
+    rc = lib.kfm_fa_bwd_blocks(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(lse), _lib.ptr(dout),
+                               _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(ws), ws_bytes, B, Nq, Nk, Hq, Hkv,
+                               D, scale, int(causal), _lib.kf_dtype(q.dtype), blocks, _lib.stream_of(q))
+    _lib.check(rc, "kfm_fa_bwd_blocks")
+    return dq, dk, dv
 
-    def force(blocks):
-        _lib.check(lib.kfm_fa_bwd_key_blocks(blocks), "kfm_fa_bwd_key_blocks")
 
-    yield force
-    force(0)
+def grads_blocks(q, k, v, cot, blocks, **kwargs):
+    """Forward, then the backward with `blocks` key blocks per dK/dV wavefront."""
+    out, lse = flash_attention(q, k, v, return_lse=True, **kwargs)
+    return bwd_blocks(cot, q, k, v, out, lse, blocks, **kwargs)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", [c for c in CASES if c[5] <= 128])
-def test_dkdv_kernels_agree(case, dtype, key_blocks):
+def test_dkdv_kernels_agree(case, dtype):
     """The two-block dK/dV kernel (32 keys per wavefront, V staged in LDS)
     against the one-block kernel and the fp64 oracle.  Per key both add the
     same products in the same order, so dK and dV agree exactly."""
     print(f"dkdv kernels case={case} dtype={dtype}", flush=True)
     q, k, v, cot = make_inputs(case, dtype, seed=7)
     kwargs = dict(causal=case[-2], softmax_scale=case[-1])
-    key_blocks(1)
-    one = hip_grads(q, k, v, cot, **kwargs)
-    key_blocks(2)
-    two = hip_grads(q, k, v, cot, **kwargs)
+    one = grads_blocks(q, k, v, cot, 1, **kwargs)
+    two = grads_blocks(q, k, v, cot, 2, **kwargs)
     ref = fp64_grads(q, k, v, cot, **kwargs)
     for name, a, b, r in zip(("dq", "dk", "dv"), one, two, ref):
         torch.testing.assert_close(b, a, atol=0, rtol=0, msg=lambda m: f"{name}: {m}")
@@ -126,7 +135,7 @@ def test_dkdv_kernels_agree(case, dtype, key_blocks):
 
 
 @pytest.mark.parametrize("d", (32, 64, 128))
-def test_dkdv_two_block_kernel_long_gqa(key_blocks, d):
+def test_dkdv_two_block_kernel_long_gqa(d):
     """Several multi-block workgroups per head (256 keys, 512 at D = 32) with a
     partial last one, GQA group of 4, causal and not: the multi-block kernel
     against the one-block kernel."""
@@ -134,10 +143,8 @@ def test_dkdv_two_block_kernel_long_gqa(key_blocks, d):
         case = (1, 700, 1100, 8, 2, d, causal, None)
         print(f"dkdv long case={case}", flush=True)
         q, k, v, cot = make_inputs(case, torch.bfloat16, seed=8)
-        key_blocks(1)
-        one = hip_grads(q, k, v, cot, causal=causal)
-        key_blocks(2)
-        two = hip_grads(q, k, v, cot, causal=causal)
+        one = grads_blocks(q, k, v, cot, 1, causal=causal)
+        two = grads_blocks(q, k, v, cot, 2, causal=causal)
         for a, b in zip(one, two):
             torch.testing.assert_close(b, a, atol=0, rtol=0)
 
@@ -177,20 +184,20 @@ def test_jvp_vjp_duality():
 
 @pytest.mark.parametrize("blocks", (1, 2))
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_deterministic_and_standalone(dtype, blocks, key_blocks):
+def test_deterministic_and_standalone(dtype, blocks):
     """Repeated backward passes give identical bits (GQA group of 4 summed in a
-    fixed order), and the standalone entry point matches autograd; with both
-    dK/dV kernels."""
-    key_blocks(blocks)
+    fixed order) with both dK/dV kernels, and the standalone entry point
+    matches autograd."""
     case = (2, 150, 170, 8, 2, 64, False, None)
     q, k, v, cot = make_inputs(case, dtype)
-    first = hip_grads(q, k, v, cot)
-    second = hip_grads(q, k, v, cot)
+    first = grads_blocks(q, k, v, cot, blocks)
+    second = grads_blocks(q, k, v, cot, blocks)
     out, lse = flash_attention(q, k, v, return_lse=True)
     standalone = flash_attention_backward(cot, q, k, v, out, lse)
-    for a, b, c in zip(first, second, standalone):
+    autograd = hip_grads(q, k, v, cot)
+    for a, b, c, d in zip(first, second, standalone, autograd):
         torch.testing.assert_close(b, a, atol=0, rtol=0)
-        torch.testing.assert_close(c, a, atol=0, rtol=0)
+        torch.testing.assert_close(c, d, atol=0, rtol=0)
     with pytest.raises(ValueError, match="lse"):
         flash_attention_backward(cot, q, k, v, out, lse.half())
     with pytest.raises(ValueError, match="dout"):
@@ -223,19 +230,18 @@ def test_baseline_config_backward(causal):
 
 
 @pytest.mark.parametrize("blocks", (1, 2))
-def test_backward_graph_replay(blocks, key_blocks):
+def test_backward_graph_replay(blocks):
     """The backward launches (dq and dkdv kernels, torch-allocated workspace)
     replay from a captured HIP graph with the eager result, also after the
     cotangent changes in place; the program's own eager work runs between
     replays.  Both dK/dV kernels."""
-    key_blocks(blocks)
     case = (1, 70, 90, 4, 2, 64, True, None)
     q, k, v, cot = make_inputs(case, torch.bfloat16)
     out, lse = flash_attention(q, k, v, causal=True, return_lse=True)
-    expected = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+    expected = bwd_blocks(cot, q, k, v, out, lse, blocks, causal=True)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        captured = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+        captured = bwd_blocks(cot, q, k, v, out, lse, blocks, causal=True)
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()
@@ -243,7 +249,7 @@ def test_backward_graph_replay(blocks, key_blocks):
             torch.testing.assert_close(c, e, atol=0, rtol=0)
         flash_attention(q, k, v)  # unrelated eager work between replays
     cot.mul_(0.5)
-    expected = flash_attention_backward(cot, q, k, v, out, lse, causal=True)
+    expected = bwd_blocks(cot, q, k, v, out, lse, blocks, causal=True)
     for _ in range(3):
         graph.replay()
         torch.cuda.synchronize()

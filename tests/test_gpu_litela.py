@@ -87,6 +87,18 @@ def test_litela_fp32_and_head_dim_16():
     _close(m(x), _module_ref(m, x, False), tol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", (torch.float32, torch.bfloat16))
+def test_litela_narrow_widths(dtype):
+    """A module whose widths are not multiples of 8 (C = 12, three heads of
+    4): both projections run on the GEMM through zero-padded operands, the
+    attention on the VALU path; the forward matches the reference."""
+    torch.manual_seed(0)
+    m = LiteLA(12, 12, dim=4, use_bias=True).to(DEV, dtype)
+    assert (m.heads, m.dim) == (3, 4)
+    x = torch.randn(2, 50, 12, generator=torch.Generator().manual_seed(6)).to(dtype).to(DEV)
+    _close(m(x), _module_ref(m, x, False), tol=1e-4 if dtype == torch.float32 else 2e-2)
+
+
 @pytest.mark.parametrize("cls", (CustomLiteLA, JointLiteLA))
 def test_custom_and_joint_modules(cls):
     torch.manual_seed(0)

@@ -45,12 +45,8 @@ CASES = [  # B, N, H
 
 @pytest.fixture(params=(3, 4), ids=("3heads", "4heads"))
 def heads_per_group(request):
-    """Both workgroup shapes (3 or 4 heads per tile), forced through the
-    library's test hook; the per-shape choice is restored afterwards."""
-    lib = _lib.load()
-    assert lib.kfm_litela_fused_heads(request.param) == 0
-    yield request.param
-    assert lib.kfm_litela_fused_heads(0) == 0
+    """Both workgroup shapes (3 or 4 heads per tile), forced per call."""
+    return request.param
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
@@ -61,7 +57,7 @@ def test_fused_matches_unfused_hip_path(dtype, bias, heads_per_group):
         x, w, b = _inputs(B, N, H, dtype, bias, 10 + i)
         xd, wd = x.to(DEV), w.to(DEV)
         bd = None if b is None else b.to(DEV)
-        got = litela_fused_attention(xd, wd, bd, H)
+        got = litela_fused_attention(xd, wd, bd, H, heads_per_group=heads_per_group)
         qkv = linear(xd, wd, bd).reshape(B, N, 3, 32 * H)
         ref = linear_attention(qkv, H, 32, 1e-15, dtype)
         torch.cuda.synchronize()
@@ -77,7 +73,8 @@ def test_fused_matches_unfused_hip_path(dtype, bias, heads_per_group):
 def test_fused_matches_the_oracle(dtype, heads_per_group):
     for i, (B, N, H) in enumerate(CASES[:4]):
         x, w, b = _inputs(B, N, H, dtype, True, 30 + i)
-        got = litela_fused_attention(x.to(DEV), w.to(DEV), b.to(DEV), H).cpu().float()
+        got = litela_fused_attention(x.to(DEV), w.to(DEV), b.to(DEV), H,
+                                     heads_per_group=heads_per_group).cpu().float()
         C = 32 * H
         qkv = (torch.nn.functional.linear(x.double(), w.double(), b.double()).to(dtype)).reshape(B, N, 3, C)
         expect = osana.linear_attention(qkv, H, 32)
@@ -88,12 +85,13 @@ def test_determinism_and_workspace_reuse(heads_per_group):
     B, N, H = 2, 300, 6
     x, w, b = _inputs(B, N, H, torch.bfloat16, True, 5)
     xd, wd, bd = x.to(DEV), w.to(DEV), b.to(DEV)
-    first = litela_fused_attention(xd, wd, bd, H)
-    second = litela_fused_attention(xd, wd, bd, H)
+    hg = dict(heads_per_group=heads_per_group)
+    first = litela_fused_attention(xd, wd, bd, H, **hg)
+    second = litela_fused_attention(xd, wd, bd, H, **hg)
     # another shape through the same workspace in between
     x2, w2, _ = _inputs(1, 513, 5, torch.bfloat16, False, 6)
-    litela_fused_attention(x2.to(DEV), w2.to(DEV), None, 5)
-    third = litela_fused_attention(xd, wd, bd, H)
+    litela_fused_attention(x2.to(DEV), w2.to(DEV), None, 5, **hg)
+    third = litela_fused_attention(xd, wd, bd, H, **hg)
     torch.cuda.synchronize()
     assert torch.equal(first, second) and torch.equal(first, third)
 

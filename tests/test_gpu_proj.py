@@ -170,6 +170,19 @@ def test_host_rejections():
     assert lib.kf_proj_gemm(null, null, null, null, 4, 12, 16, 16, 12, 0, _lib.KF_BF16, null) == 1
     assert b"multiples of 8" in lib.kf_last_error()
     assert lib.kf_proj_gemm(null, null, null, null, 0, 16, 16, 16, 16, 0, _lib.KF_BF16, null) == 0
-    with pytest.raises(ValueError, match="multiples of 8"):
-        linear(torch.zeros(3, 12, device=DEV, dtype=torch.bfloat16), torch.zeros(16, 12, device=DEV,
-                                                                                    dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("k,n", [(12, 16), (16, 12), (4, 36), (13, 7)])
+def test_ragged_widths_run_padded(k, n):
+    """Widths that are not multiples of 8 (the kernel's C ABI refuses them)
+    run on the same kernel through zero-padded copies: integer-valued inputs
+    give the exact product bit for bit, in both weight layouts, with a bias."""
+    g = torch.Generator().manual_seed(k * 100 + n)
+    x = torch.randint(-3, 4, (2, 37, k), generator=g).to(torch.bfloat16)
+    w = torch.randint(-3, 4, (n, k), generator=g).to(torch.bfloat16)
+    b = torch.randint(-3, 4, (n,), generator=g).to(torch.bfloat16)
+    exact = (x.double() @ w.double().T + b.double()).to(torch.bfloat16)
+    got = linear(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert got.shape == (2, 37, n) and got.is_contiguous()
+    assert torch.equal(got.cpu(), exact)
+    assert torch.equal(linear_t(x.to(DEV), w.t().contiguous().to(DEV), b.to(DEV)).cpu(), exact)

@@ -2,9 +2,9 @@
 
 Mirrors rmsnorm/test.py:26-63 (seeded inputs, custom vs torch module) with
 fp32 within 1e-5 relative; bf16 bit-identical to
-the oracle except for at most 1e-6 of the elements (2e-5 on the small ragged
-shapes), each within two bf16 ulps (summation-order flips of the first
-rounding point).  The module (rmsnorm/original.py:9-52) is checked with its
+the oracle except for at most 1e-5 of the elements plus a Poisson margin
+(tests/_util.py::bf16_flip_check), each within two bf16 ulps
+(summation-order flips of the first rounding point; measured 5.5e-6).  The module (rmsnorm/original.py:9-52) is checked with its
 default fp32 weight on bf16 input (an fp32 result by torch's promotion) and
 through its gradients.
 """
@@ -218,3 +218,35 @@ def test_module_gradients_through_a_residual_block():
     (x_ref + lin_ref(normed)).square().sum().backward()
     torch.testing.assert_close(x.grad.cpu().double(), x_ref.grad, atol=1e-3, rtol=1e-3)
     torch.testing.assert_close(m.weight.grad.cpu().double(), w_ref.grad, atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", (torch.float32, torch.bfloat16, torch.float16))
+def test_norm_method(dtype):
+    """``RMSNorm._norm(x)`` (rmsnorm/original.py:27-38) on the HIP kernel:
+    ``x * rsqrt(mean(x^2, -1) + eps)`` in x's dtype.  fp32: within 1e-5 of the
+    fp64 closed form; 16-bit: within one rounding of it (2^-8 relative for
+    bf16, 2^-11 for fp16), since the kernel computes in fp32 and rounds
+    once.  The rows also have unit RMS, and forward equals
+    ``_norm(x.float()).type_as(x) * weight`` (original.py:51-52)."""
+    g = torch.Generator().manual_seed(5)
+    x = (3 * torch.randn(37, 1000, generator=g)).to(dtype)
+    m = RMSNorm(1000, scale_factor=1.0, eps=1e-6).to(DEV)
+    with torch.no_grad():
+        m.weight.copy_(1 + 0.1 * torch.randn(1000, generator=g))
+    got = m._norm(x.to(DEV))
+    assert got.dtype == dtype and got.shape == x.shape
+    xd = x.double()
+    closed = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    rel = {torch.float32: 1e-5, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}[dtype]
+    torch.testing.assert_close(got.cpu().double(), closed, rtol=rel, atol=1e-30)
+    rms = got.cpu().double().pow(2).mean(-1).sqrt()
+    torch.testing.assert_close(rms, torch.ones_like(rms), rtol=4 * rel, atol=0)
+    composed = m._norm(x.to(DEV).float()).type_as(x.to(DEV)) * m.weight
+    # equal up to a summation-order flip of the 16-bit rounding point
+    torch.testing.assert_close(composed, m(x.to(DEV)), rtol=2.0 ** -7, atol=0)
+    # differentiable in x, like the reference's torch expression
+    xg = x.to(DEV).float().requires_grad_()
+    m._norm(xg).sum().backward()
+    xr = x.float().requires_grad_()
+    (xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6)).sum().backward()
+    torch.testing.assert_close(xg.grad.cpu(), xr.grad, rtol=1e-4, atol=1e-5)

@@ -53,6 +53,33 @@ def test_noalloc_matches_workspace_entry_twice(out_dtype):
             torch.testing.assert_close(out.cpu().float(), expect, atol=2e-2, rtol=2e-2)
 
 
+def test_noalloc_allocates_nothing_and_checks_clean():
+    """A warm kf_linattn_fwd_noalloc call leaves the device's free memory
+    unchanged (no allocation by the library or by torch), and
+    kf_linattn_noalloc_check finds the scratch's error word clear."""
+    lib = _lib.load()
+    B, N, H, D = 1, 2048, 16, 32
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(B, N, 3, H * D, generator=g).to(torch.bfloat16).to(DEV)
+    out = torch.empty(B, N, H * D, device=DEV, dtype=torch.bfloat16)
+    stream = _lib.stream_of(qkv)
+
+    def call():
+        _lib.check(lib.kf_linattn_fwd_noalloc(_lib.ptr(qkv), _lib.ptr(out), B, N, H, D, 0, 1e-15, _lib.KF_BF16,
+                                              _lib.KF_BF16, stream), "kf_linattn_fwd_noalloc")
+
+    call()  # warm: resolves the scratch address and loads the kernels
+    torch.cuda.synchronize()
+    free_before, _ = torch.cuda.mem_get_info()
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    free_after, _ = torch.cuda.mem_get_info()
+    assert free_after == free_before, (free_before, free_after)
+    assert lib.kf_linattn_noalloc_check(stream) == 0
+    torch.testing.assert_close(out.cpu().float(), osana.linear_attention(qkv.cpu(), H, D), atol=2e-2, rtol=2e-2)
+
+
 def test_noalloc_generic_head_dim():
     # The VALU path (head dim 64) shares the scratch the same way.
     qkv, out, ref_out = _run_both(1, 200, 4, 64, torch.float16, torch.float32, 3)
@@ -69,3 +96,6 @@ def test_noalloc_rejects_oversized_requests_before_device_work():
     rc = lib.kf_linattn_fwd_noalloc(null, null, B, N, H, D, splits, 1e-15, _lib.KF_BF16, _lib.KF_BF16, null)
     assert rc == 3  # KF_E_WORKSPACE
     assert b"static scratch" in lib.kf_last_error()
+    # invalid arguments are refused before the scratch is touched
+    assert lib.kf_linattn_fwd_noalloc(null, null, 1, 64, 2, 48, 1, 1e-15, _lib.KF_BF16, _lib.KF_BF16, null) == 1
+    assert b"dim" in lib.kf_last_error()
