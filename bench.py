@@ -279,7 +279,8 @@ def bench_proj(kind: str, B: int, N: int, C: int, steps: int, warmup: int) -> di
 def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
     """HBM stream ceiling: the library's 16-byte-per-lane copy kernel (kfm_copy,
     kernelforge_amd/csrc/measure.hip) reading and writing `nbytes` each, the
-    traffic of one RMSNorm launch; the best of 1, 2 and 4 vectors per lane."""
+    traffic of one RMSNorm launch; the best of one-wavefront blocks with one
+    vector per lane and 256-thread blocks with 1, 2 and 4."""
     from kernelforge_amd import _lib
 
     lib = _lib.load()
@@ -289,16 +290,16 @@ def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
     stream = _lib.stream_of(src[0])
     ptrs = [(_lib.ptr(src[i]), _lib.ptr(dst[i])) for i in range(n_sets)]
     best = None
-    for vpt in (1, 2, 4):
-        def launch(i, vpt=vpt):
-            rc = lib.kfm_copy(ptrs[i][0], ptrs[i][1], nbytes, vpt, stream)
+    for vpt, threads in ((1, 64), (1, 256), (2, 256), (4, 256)):
+        def launch(i, vpt=vpt, threads=threads):
+            rc = lib.kfm_copy(ptrs[i][0], ptrs[i][1], nbytes, vpt, threads, stream)
             if rc:
                 _lib.check(rc, "kfm_copy")
 
         us, n_warm = _time_launches(launch, n_sets, steps, warmup)
         if best is None or us < best["us"]:
             best = dict(repeats_us=[round(x, 3) for x in LAST_REPEATS], kernel="copy_kernel",
-                        workload=f"copy_{nbytes >> 20}MiB", vectors_per_lane=vpt,
+                        workload=f"copy_{nbytes >> 20}MiB", vectors_per_lane=vpt, threads_per_block=threads,
                         bytes=2 * nbytes, us=us, warmup_launches=n_warm, steps=steps)
     best["gbs"] = best["bytes"] / (best["us"] * 1e-6) / 1e9
     best["frac_of_peak"] = best["gbs"] / HBM_PEAK_GBS

@@ -65,7 +65,8 @@ def test_measurement_entry_points_are_exported_outside_the_header(lib):
         assert lib.kfm_fa_bwd_blocks(*bwd_args, bad, None) == KF_E_INVALID
     assert lib.kfm_litela_fused_attn_heads(None, None, None, None, None, 0, 1, 16, 2, 32, 1e-15, _lib.KF_BF16, 5,
                                            None) == KF_E_INVALID
-    assert lib.kfm_copy(None, None, 15, 1, None) == KF_E_INVALID
+    assert lib.kfm_copy(None, None, 15, 1, 64, None) == KF_E_INVALID
+    assert lib.kfm_copy(None, None, 16, 1, 128, None) == KF_E_INVALID
     # no test entry point keeps global state: the old setter hooks are gone
     for gone in ("kfm_fa_bwd_key_blocks", "kfm_litela_fused_heads", "kfm_linattn_spin_limit", "kfm_coissue",
                  "kfm_lds_rate"):
