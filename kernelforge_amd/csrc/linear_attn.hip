@@ -588,7 +588,10 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
                 const u32x4 v = *reinterpret_cast<const u32x4*>(ob + OutTile<TO>::off(tok, chunk));
                 unsigned char* dst = reinterpret_cast<unsigned char*>(out + ((int64_t)b * N + t0 + tok) * C +
                                                                       (int64_t)h0 * kD);
-                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + chunk * 16));
+                // Plain (cached) stores: 4% faster than nontemporal ones at
+                // B=1, N=16384 on MI355X (54.7 against 56.9 us), the same at
+                // B=2, N=4096; nontemporal loads stay faster for q and K/V.
+                *reinterpret_cast<u32x4*>(dst + chunk * 16) = v;
             }
         }
     };
