@@ -306,6 +306,54 @@ def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
     return best
 
 
+def bench_copy_sweep(steps: int, warmup: int) -> dict:
+    """Stream-ceiling sweep behind the copy ceiling (kfm_copy_ex): at the
+    three RMSNorm traffic sizes (64, 128 and 256 MiB read and written), every
+    block size (64, 256, 1024 threads) x vectors per lane (1, 2, 4, 8) x cache
+    policy (nontemporal or plain loads and stores), then the fastest shape of
+    each size with dynamic LDS capping the blocks per CU.  Microseconds per
+    launch and the fraction of 8 TB/s; the best entry per size."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    policies = {0: "nt/nt", 1: "plain/nt", 2: "nt/plain", 3: "plain/plain"}
+    out = {}
+    for nbytes in (16384 * 2048 * 2, 16384 * 4096 * 2, 16384 * 8192 * 2):
+        n_sets = _sets_for(2 * nbytes)
+        src = [torch.empty(nbytes // 2, device="cuda", dtype=torch.bfloat16).normal_() for _ in range(n_sets)]
+        dst = [torch.empty_like(x) for x in src]
+        stream = _lib.stream_of(src[0])
+        ptrs = [(_lib.ptr(src[i]), _lib.ptr(dst[i])) for i in range(n_sets)]
+
+        def run(vpt, threads, pol, lds):
+            # A one-block copy first: it separates consecutive configurations
+            # of the same kernel and grid in a kernel trace.
+            _lib.check(lib.kfm_copy_ex(ptrs[0][0], ptrs[0][1], 16, 1, 64, 0, 0, stream), "kfm_copy_ex")
+
+            def launch(i):
+                rc = lib.kfm_copy_ex(ptrs[i][0], ptrs[i][1], nbytes, vpt, threads, pol, lds, stream)
+                if rc:
+                    _lib.check(rc, "kfm_copy_ex")
+
+            us, _ = _time_launches(launch, n_sets, steps, warmup)
+            return dict(threads=threads, vectors_per_lane=vpt, policy=policies[pol], lds_bytes=lds,
+                        us=round(us, 3), frac_of_peak=round(2 * nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+
+        rows = [run(vpt, threads, pol, 0) for threads in (64, 256, 1024) for vpt in (1, 2, 4, 8)
+                for pol in (0, 1, 2, 3)]
+        best = min(rows, key=lambda r: r["us"])
+        # Occupancy caps for the fastest shape: blocks per CU limited to about
+        # 160 KiB / lds_bytes.
+        for lds in (5 * 1024, 10 * 1024, 20 * 1024, 40 * 1024):
+            rows.append(run(best["vectors_per_lane"], best["threads"],
+                            {v: k for k, v in policies.items()}[best["policy"]], lds))
+        best = min(rows, key=lambda r: r["us"])
+        out[f"copy_{nbytes >> 20}MiB"] = dict(bytes=2 * nbytes, best=best, rows=rows)
+        print(f"# copy sweep {nbytes >> 20} MiB: best {best}", file=sys.stderr, flush=True)
+        del src, dst
+    return dict(kernel="copy_kernel", workload="copy_sweep", us=0.0, sizes=out)
+
+
 def bench_mfma(warmup: int) -> dict:
     """Dense bf16 MFMA ceiling: kfm_mfma_bf16 (two independent
     v_mfma_f32_32x32x16_bf16 chains per wavefront) at 1, 2 and 4 wavefronts
@@ -495,7 +543,8 @@ def main() -> int:
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
                          "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|copy2048|copy4096|copy8192|mfma), e.g. under "
-                         "rocprofv3, or a hardware probe (coissue|lds_rate) that the default run skips")
+                         "rocprofv3, or a probe that the default run skips (coissue|lds_rate: issue rates; "
+                         "copy_sweep: the stream-ceiling sweep)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
                     help="GPU time of untimed launches after the warm-up steps (clock settling)")
@@ -532,6 +581,7 @@ def main() -> int:
     # default run does not.
     probes = {
         "coissue": lambda: bench_coissue(warmup),
+        "copy_sweep": lambda: bench_copy_sweep(min(steps, 50), warmup),
         "lds_rate": lambda: bench_lds_rate(warmup),
     }
     if args.only:

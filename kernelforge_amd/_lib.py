@@ -98,6 +98,7 @@ SIGNATURES = {
 # by the library, not part of the public header.
 MEASURE_SIGNATURES = {
     "kfm_copy": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _c_void_p]),
+    "kfm_copy_ex": (_int, [_c_void_p, _c_void_p, _i64, _int, _int, _int, _int, _c_void_p]),
     "kfm_mfma_bf16": (_int, [_c_void_p, _i64, _int, _c_void_p]),
     "kfm_litela_fused_attn_heads": (
         _int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _f32, _int,

@@ -11,39 +11,85 @@ namespace {
 // Stream copy: thread t of a block of BS threads moves the 16-byte vectors
 // (b * VPT + i) * BS + t, i < VPT, so every load and store instruction of a
 // wavefront covers one contiguous 1 KiB span, the access shape of the
-// RMSNorm kernel.  All VPT loads are issued before the first store.  On
-// MI355X one-wavefront blocks with one vector per lane stream fastest (3-5%
-// above 256-thread blocks at 64-256 MiB; more vectors per lane, larger
-// blocks and other block-to-XCD orders were slower).
-template <int VPT, int BS>
+// RMSNorm kernel.  All VPT loads are issued before the first store.  POL
+// selects the cache policy: bit 0 plain (cached) loads instead of
+// nontemporal ones, bit 1 plain stores.  On MI355X one-wavefront blocks with
+// one vector per lane and nontemporal loads and stores stream fastest (3-5%
+// above 256-thread blocks at 64-256 MiB; the sweep of `bench.py --only
+// copy_sweep` covers block sizes, vectors per lane, cache policies and
+// occupancy limits).
+template <int VPT, int BS, int POL = 0>
 __global__ __launch_bounds__(BS) void copy_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
                                                   int64_t nvec) {
     const int64_t base = (int64_t)blockIdx.x * BS * VPT + threadIdx.x;
+    const u32x4* s = src + base;
+    u32x4* d = dst + base;
     u32x4 v[VPT];
+    if (base + (int64_t)(VPT - 1) * BS < nvec) {
+        // Whole block in range: no per-vector guards (they cost registers).
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int64_t j = base + (int64_t)i * BS;
-        v[i] = j < nvec ? __builtin_nontemporal_load(src + j) : u32x4{0u, 0u, 0u, 0u};
+        for (int i = 0; i < VPT; ++i) v[i] = (POL & 1) ? s[i * BS] : __builtin_nontemporal_load(s + i * BS);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            if constexpr (POL & 2) d[i * BS] = v[i];
+            else __builtin_nontemporal_store(v[i], d + i * BS);
+        }
+        return;
     }
-#pragma unroll
     for (int i = 0; i < VPT; ++i) {
-        const int64_t j = base + (int64_t)i * BS;
-        if (j < nvec) __builtin_nontemporal_store(v[i], dst + j);
+        if (base + (int64_t)i * BS >= nvec) break;
+        const u32x4 x = (POL & 1) ? s[i * BS] : __builtin_nontemporal_load(s + i * BS);
+        if constexpr (POL & 2) d[i * BS] = x;
+        else __builtin_nontemporal_store(x, d + i * BS);
     }
 }
 
-template <int BS>
-int launch_copy(int vpt, const u32x4* in, u32x4* o, int64_t nvec, hipStream_t s) {
+// Dynamic LDS of `lds` bytes per block limits the blocks a CU holds at once.
+template <int BS, int POL>
+int launch_copy(int vpt, const u32x4* in, u32x4* o, int64_t nvec, int lds, hipStream_t s) {
     const int64_t blocks = (nvec + (int64_t)BS * vpt - 1) / ((int64_t)BS * vpt);
     KF_REQUIRE(blocks <= 0x7fffffff, KF_E_UNSUPPORTED, "copy: too many blocks");
+    const dim3 g((unsigned)blocks), b(BS);
     switch (vpt) {
-        case 1: hipLaunchKernelGGL((copy_kernel<1, BS>), dim3((unsigned)blocks), dim3(BS), 0, s, in, o, nvec); break;
-        case 2: hipLaunchKernelGGL((copy_kernel<2, BS>), dim3((unsigned)blocks), dim3(BS), 0, s, in, o, nvec); break;
-        case 4: hipLaunchKernelGGL((copy_kernel<4, BS>), dim3((unsigned)blocks), dim3(BS), 0, s, in, o, nvec); break;
-        case 8: hipLaunchKernelGGL((copy_kernel<8, BS>), dim3((unsigned)blocks), dim3(BS), 0, s, in, o, nvec); break;
+        case 1: hipLaunchKernelGGL((copy_kernel<1, BS, POL>), g, b, lds, s, in, o, nvec); break;
+        case 2: hipLaunchKernelGGL((copy_kernel<2, BS, POL>), g, b, lds, s, in, o, nvec); break;
+        case 4: hipLaunchKernelGGL((copy_kernel<4, BS, POL>), g, b, lds, s, in, o, nvec); break;
+        case 8: hipLaunchKernelGGL((copy_kernel<8, BS, POL>), g, b, lds, s, in, o, nvec); break;
         default: set_error("copy: vectors_per_thread must be 1, 2, 4 or 8, got %d", vpt); return KF_E_INVALID;
     }
     return check_launch("copy_kernel launch");
+}
+
+template <int POL>
+int launch_copy_bs(int bs, int vpt, const u32x4* in, u32x4* o, int64_t nvec, int lds, hipStream_t s) {
+    switch (bs) {
+        case 64: return launch_copy<64, POL>(vpt, in, o, nvec, lds, s);
+        case 256: return launch_copy<256, POL>(vpt, in, o, nvec, lds, s);
+        case 1024: return launch_copy<1024, POL>(vpt, in, o, nvec, lds, s);
+    }
+    set_error("copy: threads_per_block must be 64, 256 or 1024, got %d", bs);
+    return KF_E_INVALID;
+}
+
+int copy_run(const void* src, void* dst, int64_t bytes, int vpt, int bs, int policy, int lds, hipStream_t s) {
+    KF_REQUIRE(bytes >= 0 && bytes % 16 == 0, KF_E_INVALID, "copy: bytes %lld not a multiple of 16",
+               (long long)bytes);
+    KF_REQUIRE(bytes == 0 || (src && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0),
+               KF_E_INVALID, "copy: null or unaligned pointer");
+    KF_REQUIRE(bs == 64 || bs == 256 || bs == 1024, KF_E_INVALID,
+               "copy: threads_per_block must be 64, 256 or 1024, got %d", bs);
+    KF_REQUIRE(policy >= 0 && policy <= 3, KF_E_INVALID, "copy: policy must be 0..3, got %d", policy);
+    KF_REQUIRE(lds >= 0 && lds <= 65536, KF_E_INVALID, "copy: lds_bytes must be 0..65536, got %d", lds);
+    if (bytes == 0) return KF_OK;
+    const int64_t nvec = bytes / 16;
+    const u32x4* in = static_cast<const u32x4*>(src);
+    u32x4* o = static_cast<u32x4*>(dst);
+    switch (policy) {
+        case 0: return launch_copy_bs<0>(bs, vpt, in, o, nvec, lds, s);
+        case 1: return launch_copy_bs<1>(bs, vpt, in, o, nvec, lds, s);
+        case 2: return launch_copy_bs<2>(bs, vpt, in, o, nvec, lds, s);
+        default: return launch_copy_bs<3>(bs, vpt, in, o, nvec, lds, s);
+    }
 }
 
 // Dense bf16 MFMA issue rate: each wavefront runs `iters` rounds of two
@@ -81,19 +127,19 @@ __global__ __launch_bounds__(256) void mfma_kernel(float* __restrict__ out, int 
 extern "C" int kfm_copy(const void* src, void* dst, int64_t bytes, int vectors_per_thread, int threads_per_block,
                         kf_stream_t stream) {
     using namespace kf;
-    KF_REQUIRE(bytes >= 0 && bytes % 16 == 0, KF_E_INVALID, "copy: bytes %lld not a multiple of 16",
-               (long long)bytes);
-    KF_REQUIRE(bytes == 0 || (src && dst && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0),
-               KF_E_INVALID, "copy: null or unaligned pointer");
     KF_REQUIRE(threads_per_block == 64 || threads_per_block == 256, KF_E_INVALID,
                "copy: threads_per_block must be 64 or 256, got %d", threads_per_block);
-    if (bytes == 0) return KF_OK;
-    const int64_t nvec = bytes / 16;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const u32x4* in = static_cast<const u32x4*>(src);
-    u32x4* o = static_cast<u32x4*>(dst);
-    return threads_per_block == 64 ? launch_copy<64>(vectors_per_thread, in, o, nvec, s)
-                                   : launch_copy<256>(vectors_per_thread, in, o, nvec, s);
+    return copy_run(src, dst, bytes, vectors_per_thread, threads_per_block, 0, 0, static_cast<hipStream_t>(stream));
+}
+
+// The copy with every variable of the ceiling sweep: threads_per_block 64,
+// 256 or 1024; policy bit 0 = plain loads, bit 1 = plain stores (else
+// nontemporal); lds_bytes of dynamic LDS per block (0..65536) to cap the
+// blocks per CU.
+extern "C" int kfm_copy_ex(const void* src, void* dst, int64_t bytes, int vectors_per_thread, int threads_per_block,
+                           int policy, int lds_bytes, kf_stream_t stream) {
+    return kf::copy_run(src, dst, bytes, vectors_per_thread, threads_per_block, policy, lds_bytes,
+                        static_cast<hipStream_t>(stream));
 }
 
 // Run the MFMA loop on `blocks` blocks of 256 threads for `iters` rounds;

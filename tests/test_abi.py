@@ -67,6 +67,9 @@ def test_measurement_entry_points_are_exported_outside_the_header(lib):
                                            None) == KF_E_INVALID
     assert lib.kfm_copy(None, None, 15, 1, 64, None) == KF_E_INVALID
     assert lib.kfm_copy(None, None, 16, 1, 128, None) == KF_E_INVALID
+    assert lib.kfm_copy_ex(None, None, 16, 1, 64, 4, 0, None) == KF_E_INVALID
+    assert lib.kfm_copy_ex(None, None, 16, 1, 64, 0, 65537, None) == KF_E_INVALID
+    assert lib.kfm_copy_ex(None, None, 0, 1, 1024, 3, 65536, None) == 0
     # no test entry point keeps global state: the old setter hooks are gone
     for gone in ("kfm_fa_bwd_key_blocks", "kfm_litela_fused_heads", "kfm_linattn_spin_limit", "kfm_coissue",
                  "kfm_lds_rate"):
