@@ -276,6 +276,60 @@ def bench_proj(kind: str, B: int, N: int, C: int, steps: int, warmup: int) -> di
                 library_tflops=flops / (lib_us * 1e-6) / 1e12)
 
 
+def bench_litela(B: int, N: int, H: int, steps: int, warmup: int) -> dict:
+    """LiteLA attention with the QKV projection fused in (kf_litela_fused_attn:
+    x[B, N, 32H] -> the attention output before the output projection, q, k
+    and v never written to HBM), head dim 32, bf16.  The unfused pair -- the
+    projection GEMM (kf_proj_gemm) into a packed qkv, then kf_linattn_fwd --
+    is timed beside it as "unfused_us".  Flops: the projection's 2 M 3C C plus
+    the attention's 4 B H N D (D + 1); the projection dominates, so the
+    roofline is the dense bf16 MFMA peak."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    D, C = 32, 32 * H
+    M = B * N
+    g = _gen(13)
+    w = (torch.randn(3 * C, C, generator=g) / C ** 0.5).to(torch.bfloat16).to("cuda")
+    n_sets = _sets_for(M * C * 2 * 5)
+    xs = [torch.randn(B, N, C, generator=g).to(torch.bfloat16).to("cuda") for _ in range(n_sets)]
+    outs = [torch.empty(B, N, C, device="cuda", dtype=torch.bfloat16) for _ in range(n_sets)]
+    stream = _lib.stream_of(xs[0])
+    wsb = lib.kf_litela_fused_workspace_bytes(B, N, H)
+    ws = torch.empty(max(wsb, 256), device="cuda", dtype=torch.uint8)
+
+    def fused(i):
+        rc = lib.kf_litela_fused_attn(_lib.ptr(xs[i]), _lib.ptr(w), None, _lib.ptr(outs[i]), _lib.ptr(ws), wsb,
+                                      B, N, H, D, 1e-15, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_litela_fused_attn")
+
+    us, n_warm = _time_launches(fused, n_sets, steps, warmup)
+    repeats = list(LAST_REPEATS)
+    qkv = torch.empty(B, N, 3 * C, device="cuda", dtype=torch.bfloat16)
+    splits = lib.kf_linattn_default_splits(B, H, D, N)
+    lwsb = lib.kf_linattn_workspace_bytes(B, H, D, splits)
+    lws = torch.zeros(max(lwsb, 256), device="cuda", dtype=torch.uint8)
+
+    def unfused(i):
+        rc = lib.kf_proj_gemm(_lib.ptr(xs[i]), _lib.ptr(w), None, _lib.ptr(qkv), M, 3 * C, C, C, 3 * C,
+                              _lib.KF_WEIGHT_NK, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_proj_gemm")
+        rc = lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(outs[i]), _lib.ptr(lws), lwsb, B, N, H, D, splits, 1e-15,
+                                _lib.KF_BF16, _lib.KF_BF16, stream)
+        if rc:
+            _lib.check(rc, "kf_linattn_fwd")
+
+    unfused_us, _ = _time_launches(unfused, n_sets, steps, warmup)
+    flops = 2 * M * 3 * C * C + 4 * B * H * N * D * (D + 1)
+    tflops = flops / (us * 1e-6) / 1e12
+    return dict(repeats_us=[round(x, 3) for x in repeats], kernel="litela_fused",
+                workload=f"litela_fused_bf16_B{B}_H{H}_N{N}", us=us, flops=flops, warmup_launches=n_warm,
+                steps=steps, sets=n_sets, tflops=tflops, roofline_frac=tflops / BF16_PEAK_TFLOPS,
+                unfused_us=unfused_us, speedup_vs_unfused=unfused_us / us)
+
+
 def bench_copy(nbytes: int, steps: int, warmup: int) -> dict:
     """HBM stream ceiling: the library's 16-byte-per-lane copy kernel (kfm_copy,
     kernelforge_amd/csrc/measure.hip) reading and writing `nbytes` each, the
@@ -542,7 +596,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default=None,
                     help="run one workload only (rmsnorm2048|rmsnorm4096|rmsnorm8192|sanaA|sanaB|"
-                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|copy2048|copy4096|copy8192|mfma), e.g. under "
+                         "fa_fwd_jvp|fa_jvp|fa_fwd|fa_bwd|proj_qkvA|proj_outA|litela_fusedA|copy2048|copy4096|copy8192|mfma), "
+                         "e.g. under "
                          "rocprofv3, or a probe that the default run skips (coissue|lds_rate: issue rates; "
                          "copy_sweep: the stream-ceiling sweep)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -572,6 +627,7 @@ def main() -> int:
         "fa_bwd": lambda: bench_fa("bwd", max(10, steps // 5), max(3, warmup // 2)),
         "proj_qkvA": lambda: bench_proj("qkv", 2, 4096, 2240, steps, warmup),
         "proj_outA": lambda: bench_proj("out", 2, 4096, 2240, steps, warmup),
+        "litela_fusedA": lambda: bench_litela(2, 4096, 70, steps, warmup),
         "copy2048": lambda: bench_copy(16384 * 2048 * 2, steps, warmup),
         "copy4096": lambda: bench_copy(16384 * 4096 * 2, steps, warmup),
         "copy8192": lambda: bench_copy(16384 * 8192 * 2, steps, warmup),
