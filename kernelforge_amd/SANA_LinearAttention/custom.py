@@ -92,7 +92,10 @@ def _launch(kind: str, qkv: torch.Tensor, out: torch.Tensor, B: int, N: int, hea
         splits = int(lib.kf_linattn_default_splits(B, heads, dim, N))
     if splits < 1:
         raise ValueError(f"splits must be positive, got {splits}")
-    ws_bytes = int(lib.kf_linattn_workspace_bytes(B, heads, dim, splits))
+    # The library runs at most one split per 32-token tile (its smallest split
+    # unit), so a larger request needs no larger workspace.
+    ws_splits = min(splits, max(1, -(-N // 32)))
+    ws_bytes = int(lib.kf_linattn_workspace_bytes(B, heads, dim, ws_splits))
     ws = _workspace(qkv.device, ws_bytes)
     stream = _lib.stream_of(qkv)
     if kind == "fwd":
