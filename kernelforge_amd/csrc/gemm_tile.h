@@ -13,7 +13,10 @@
 //
 // Workgroup: WAVES wavefronts, a BM x BN output tile, K streamed through LDS
 // in stages of 64- or 128-byte rows by global_load_lds copies (no register
-// staging), STAGES buffers deep.  Each wavefront owns a WM x WN sub-tile.  A
+// staging), STAGES buffers deep.  Copies of whole stages of in-range rows take
+// a scalar base per instruction and one per-lane offset per wavefront, so
+// they cost no vector instructions; others compute a clamped address per lane.
+// Each wavefront owns a WM x WN sub-tile.  A
 // lane reads one 16-byte chunk per operand block and 64-byte K step: one
 // v_mfma_f32_16x16x32 for bf16/f16, four v_mfma_f32_16x16x4f32 for fp32, whose
 // K slices are taken as {4g + t} so that the same chunk read serves all four.
@@ -190,6 +193,15 @@ template <typename T> __device__ __forceinline__ f32x4 mma_chunk(u32x4 a, u32x4 
     }
 }
 
+// Workgroup barrier once this wavefront's LDS operations have completed;
+// its outstanding LDS copies (vmcnt) are not waited for.
+__device__ __forceinline__ void barrier_lds() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // s_waitcnt vmcnt(N) with the expcnt / lgkmcnt fields left at their maxima.
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
@@ -222,25 +234,112 @@ template <typename T> struct GemmSrc {
     const T* w;
     int K;
     int n0, N;  // KN only
+    // NK only: wrow(RPC b + j) == wrow(RPC b) + j for every block b of RPC
+    // tile rows (j < RPC), so each copy instruction reads RPC consecutive
+    // weight rows and can take a scalar base.
+    bool w_rows_linear = false;
 };
+
+// Lane byte offset of the scalar-base copies of a K-contiguous [R][BK] tile
+// from rows of stride ld: wavefront w issues instructions i = w + WAVES j,
+// whose lanes cover tile row RPC i + lane/CPR at logical chunk
+// (lane%CPR) ^ kswz(row).  WAVES * RPC is a multiple of 16, so that swizzle
+// is the same for every instruction of a wavefront and one offset serves all.
+template <typename T, typename C>
+__device__ __forceinline__ uint32_t krows_lane_off(int64_t ld, int wave, int lane) {
+    static_assert((C::WAVES * C::RPC) % 16 == 0, "one swizzle per wavefront");
+    const int r = C::RPC * wave + lane / C::CPR;
+    const int c = (lane % C::CPR) ^ kswz<C::CPR>(r);
+    return (uint32_t)((int64_t)(lane / C::CPR) * ld * (int64_t)sizeof(T) + c * 16);
+}
+
+// Whole-stage copy (K columns k0..k0+BK-1, all < K) of tile rows 0..R-1 whose
+// instruction i reads the RPC consecutive rows starting at rowbase(RPC i)
+// (stride ld): a scalar base per instruction plus the wavefront's lane
+// offset (krows_lane_off); tile_lds is the tile's LDS byte address and wave
+// a wavefront-uniform value.
+template <typename T, typename C, int R, typename RowBase>
+__device__ __forceinline__ void copy_krows_sbase(uint32_t tile_lds, RowBase rowbase, uint32_t voff, int k0,
+                                                 int wave) {
+    constexpr int NI = R / C::RPC;
+#pragma unroll
+    for (int j = 0; j < (NI + C::WAVES - 1) / C::WAVES; ++j) {
+        const int i = wave + C::WAVES * j;
+        if (NI % C::WAVES != 0 && i >= NI) break;
+        lds_copy16_sbase(rowbase(C::RPC * i) + k0, voff, tile_lds + (uint32_t)(C::RPC * i * C::BK * (int)sizeof(T)));
+    }
+}
 
 // Accumulate one wavefront's WM x WN sub-tile over the whole K range.
 // acc[nb][mb][i] = y[m = wm*WM + 16 mb + l%16][n = wn*WN + 16 nb + 4(l/16) + i].
+//
+// Loop schedule: the K range is a sequence of MFMA steps (STEPS per stage),
+// and the operand chunks of step q+1 are read from LDS while step q's MFMAs
+// run, across stage boundaries too.  Before the first read of stage t each
+// wavefront waits for its own copies of stage t and meets the others at one
+// barrier; after it stage t-1's buffer is free (every read of it has
+// completed), so the copies of stage t + STAGES - 1 go there.  The two
+// operand sets alternate between even and odd steps.  A second operand set
+// is live throughout, so sub-tiles of more than 28 16x16 blocks (BN = 256,
+// which then spills) read each step's operands just before its MFMAs.
 template <typename T, typename C, typename WRow>
 __device__ __forceinline__ void gemm_mainloop(const GemmSrc<T>& src, WRow wrow, T* lds, int wave, int lane,
                                               f32x4 (&acc)[C::NB][C::MB]) {
     constexpr int PER = C::XI + C::WI;
+    constexpr bool kPrefetch = C::NB * C::MB <= 28;
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     const int KT = (src.K + C::BK - 1) / C::BK;
     const int64_t xr0 = src.x_row0, xlast = src.x_rows_end - 1;
     auto xrow = [xr0, xlast](int r) { return min(xr0 + r, xlast); };
 
+    // Scalar-base copies of whole stages when the tile's activation rows are
+    // all in range and its weight rows are linear in 8-row blocks.
+    const int swave = __builtin_amdgcn_readfirstlane(wave);
+    const bool fast = !C::KN && src.w_rows_linear && xr0 + C::BM <= src.x_rows_end;
+    const uint32_t x_voff = krows_lane_off<T, C>(src.ldx, swave, lane);
+    const uint32_t w_voff = krows_lane_off<T, C>(src.K, swave, lane);
+    const uint32_t lds0 = lds_addr(lds);
+    const T* xg = src.x + xr0 * src.ldx;
+    auto xbase = [xg, &src](int r) { return xg + (int64_t)r * src.ldx; };
+    auto wbase = [&src, &wrow](int r) { return src.w + wrow(r) * (int64_t)src.K; };
+
     auto issue = [&](int kt) {
-        T* xs = lds + (kt % C::STAGES) * (C::XS + C::WS);
+        const int buf = kt % C::STAGES;
+        if (fast && (kt + 1) * C::BK <= src.K) {
+            const uint32_t xl = lds0 + (uint32_t)(buf * (C::XS + C::WS) * (int)sizeof(T));
+            copy_krows_sbase<T, C, C::BM>(xl, xbase, x_voff, kt * C::BK, swave);
+            copy_krows_sbase<T, C, C::BN>(xl + C::XS * (uint32_t)sizeof(T), wbase, w_voff, kt * C::BK, swave);
+            return;
+        }
+        T* xs = lds + buf * (C::XS + C::WS);
         T* ws = xs + C::XS;
         copy_krows<T, C, C::BM>(xs, src.x, src.ldx, xrow, kt * C::BK, src.K, wave, lane);
         if constexpr (C::KN) copy_kn<T, C>(ws, src.w, src.N, src.n0, kt * C::BK, src.K, wave, lane);
         else copy_krows<T, C, C::BN>(ws, src.w, src.K, wrow, kt * C::BK, src.K, wave, lane);
+    };
+    auto read_ops = [&](int kt, int s, u32x4 (&a)[C::NB], u32x4 (&b)[C::MB]) {
+        const T* xs = lds + (kt % C::STAGES) * (C::XS + C::WS);
+        const T* ws = xs + C::XS;
+#pragma unroll
+        for (int nb = 0; nb < C::NB; ++nb) {
+            if constexpr (C::KN) a[nb] = op_kn<T, C>(ws, wn * C::WN + 16 * nb, s, lane);
+            else a[nb] = op_krows<T, C>(ws, wn * C::WN + 16 * nb, s, lane);
+        }
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) b[mb] = op_krows<T, C>(xs, wm * C::WM + 16 * mb, s, lane);
+    };
+    auto mma_step = [&](const u32x4 (&a)[C::NB], const u32x4 (&b)[C::MB]) {
+#pragma unroll
+        for (int nb = 0; nb < C::NB; ++nb)
+#pragma unroll
+            for (int mb = 0; mb < C::MB; ++mb) acc[nb][mb] = mma_chunk<T>(a[nb], b[mb], acc[nb][mb]);
+    };
+    // Stage t's copies have landed for every wavefront; stage t-1's buffer
+    // takes stage t + STAGES - 1.
+    auto enter_stage = [&](int t) {
+        wait_stage<C::STAGES, PER>(min(C::STAGES - 2, KT - 1 - t));
+        barrier_lds();
+        if (t + C::STAGES - 1 < KT) issue(t + C::STAGES - 1);
     };
 
 #pragma unroll
@@ -252,26 +351,35 @@ __device__ __forceinline__ void gemm_mainloop(const GemmSrc<T>& src, WRow wrow, 
     for (int s = 0; s < C::STAGES - 1; ++s)
         if (s < KT) issue(s);
 
-    for (int kt = 0; kt < KT; ++kt) {
-        wait_stage<C::STAGES, PER>(min(C::STAGES - 2, KT - 1 - kt));
-        __syncthreads();  // stage kt is complete for every wavefront; stage kt-1 is free
-        if (kt + C::STAGES - 1 < KT) issue(kt + C::STAGES - 1);
-        const T* xs = lds + (kt % C::STAGES) * (C::XS + C::WS);
-        const T* ws = xs + C::XS;
-#pragma unroll
-        for (int s = 0; s < C::STEPS; ++s) {
-            u32x4 a[C::NB], b[C::MB];
-#pragma unroll
-            for (int nb = 0; nb < C::NB; ++nb) {
-                if constexpr (C::KN) a[nb] = op_kn<T, C>(ws, wn * C::WN + 16 * nb, s, lane);
-                else a[nb] = op_krows<T, C>(ws, wn * C::WN + 16 * nb, s, lane);
+    if constexpr (kPrefetch) {
+        const int TS = KT * C::STEPS;
+        // Read step q's operands into (a, b), entering its stage first when q
+        // is the stage's first step.
+        static_assert(C::STEPS == 1 || C::STEPS == 2, "steps per stage");
+        auto prepare = [&](int q, u32x4 (&a)[C::NB], u32x4 (&b)[C::MB]) {
+            const int t = C::STEPS == 1 ? q : q >> 1, s = C::STEPS == 1 ? 0 : q & 1;
+            if (s == 0) enter_stage(t);
+            read_ops(t, s, a, b);
+        };
+        u32x4 a0[C::NB], b0[C::MB], a1[C::NB], b1[C::MB];
+        prepare(0, a0, b0);
+        for (int q = 0; q < TS; q += 2) {
+            if (q + 1 < TS) prepare(q + 1, a1, b1);
+            mma_step(a0, b0);
+            if (q + 1 < TS) {
+                if (q + 2 < TS) prepare(q + 2, a0, b0);
+                mma_step(a1, b1);
             }
+        }
+    } else {
+        for (int kt = 0; kt < KT; ++kt) {
+            enter_stage(kt);
 #pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb) b[mb] = op_krows<T, C>(xs, wm * C::WM + 16 * mb, s, lane);
-#pragma unroll
-            for (int nb = 0; nb < C::NB; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < C::MB; ++mb) acc[nb][mb] = mma_chunk<T>(a[nb], b[mb], acc[nb][mb]);
+            for (int s = 0; s < C::STEPS; ++s) {
+                u32x4 a[C::NB], b[C::MB];
+                read_ops(kt, s, a, b);
+                mma_step(a, b);
+            }
         }
     }
 }

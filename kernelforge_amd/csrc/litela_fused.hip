@@ -117,7 +117,8 @@ void litela_kv_state_kernel(FusedLaParams p) {
     f32x4 acc[Cf::NB][Cf::MB];
     {
         const int64_t row0 = (int64_t)b * p.N + t0;
-        const GemmSrc<T> src{x, C, row0, (int64_t)b * p.N + p.N, w, p.C, 0, 0};
+        GemmSrc<T> src{x, C, row0, (int64_t)b * p.N + p.N, w, p.C, 0, 0};
+        src.w_rows_linear = true;  // 8-row blocks stay inside one head's 32 rows of k or v
         const int hlast = p.H - 1;
         auto wrow = [C, h0, hlast](int r) {
             const int part = r >= KW ? 1 : 0, rr = r - part * KW;
@@ -253,7 +254,8 @@ void litela_q_out_kernel(FusedLaParams p) {
     f32x4 acc[Cf::NB][Cf::MB];
     {
         const int64_t row0 = (int64_t)b * p.N + t0;
-        const GemmSrc<T> src{x, C, row0, (int64_t)b * p.N + p.N, w, p.C, 0, 0};
+        GemmSrc<T> src{x, C, row0, (int64_t)b * p.N + p.N, w, p.C, 0, 0};
+        src.w_rows_linear = true;  // 8-row blocks stay inside one head's 32 rows of q
         const int hlast = p.H - 1;
         auto wrow = [h0, hlast](int r) { return (int64_t)min(h0 + (r >> 5), hlast) * kHD + (r & 31); };
         gemm_mainloop<T, Cf>(src, wrow, lds, wave, lane, acc);

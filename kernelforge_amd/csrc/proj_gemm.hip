@@ -18,6 +18,7 @@ struct GemmParams {
     int M, N, K;
     int64_t ldx, ldy;
     int tiles_m, tiles_n;
+    int staged_out;  // y and its row stride are 16-byte aligned: whole-chunk stores
 };
 
 // Logical block -> (tile row, tile column), kGroupM tile rows per column step:
@@ -32,6 +33,15 @@ __device__ __forceinline__ void gemm_tile(int blk, int tiles_m, int tiles_n, int
     tn = r / gm;
 }
 
+// Output tile staged in the (then free) stage buffers: rows of BN elements
+// plus 16 bytes, so the 16 rows one 8- or 16-byte staging write touches fall
+// on different banks.
+template <typename T, typename C> struct StagedOut {
+    static constexpr int ROWE = C::BN + 16 / (int)sizeof(T);     // elements per staged row
+    static constexpr int CHUNKS = C::BN * (int)sizeof(T) / 16;    // 16-byte chunks per output row
+    static constexpr bool FITS = C::BM * ROWE <= C::STAGES * (C::XS + C::WS);
+};
+
 template <typename T, typename C, bool BIAS>
 __global__ __launch_bounds__(C::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void proj_gemm_kernel(GemmParams p) {
@@ -42,12 +52,53 @@ void proj_gemm_kernel(GemmParams p) {
     const int m0 = tm * C::BM, n0 = tn * C::BN;
 
     f32x4 acc[C::NB][C::MB];
-    const GemmSrc<T> src{static_cast<const T*>(p.x), p.ldx, m0, p.M, static_cast<const T*>(p.w), p.K, n0, p.N};
+    GemmSrc<T> src{static_cast<const T*>(p.x), p.ldx, m0, p.M, static_cast<const T*>(p.w), p.K, n0, p.N};
+    src.w_rows_linear = n0 + C::BN <= p.N;  // no clamped weight rows in this tile
     const int nlast = p.N - 1;
     gemm_mainloop<T, C>(src, [n0, nlast](int r) { return (int64_t)min(n0 + r, nlast); }, lds, wave, lane, acc);
 
     const int wm = wave / C::WAVES_N, wn = wave % C::WAVES_N;
     T* y = static_cast<T*>(p.y);
+    typedef StagedOut<T, C> SO;
+    if constexpr (SO::FITS) {
+        if (p.staged_out) {
+            // Round (+ bias) into the staged tile, then store whole rows in
+            // 16-byte chunks: full cache lines instead of the 32-byte row
+            // pieces one MFMA block holds (which wrote 1.5x the output's
+            // bytes at N = 2240).
+            __syncthreads();  // every wavefront is done with the stage buffers
+#pragma unroll
+            for (int nb = 0; nb < C::NB; ++nb) {
+                const int nl = wn * C::WN + 16 * nb + 4 * (lane >> 4);
+                float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                if constexpr (BIAS) {
+                    if (n0 + nl < p.N) {
+                        const T* bias = static_cast<const T*>(p.bias) + n0 + nl;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) bv[i] = to_f32(bias[i]);
+                    }
+                }
+#pragma unroll
+                for (int mb = 0; mb < C::MB; ++mb) {
+                    const int ml = wm * C::WM + 16 * mb + (lane & 15);
+                    store4(lds + ml * SO::ROWE + nl, acc[nb][mb], bv);
+                }
+            }
+            __syncthreads();
+            constexpr int TOTAL = C::BM * SO::CHUNKS;
+#pragma unroll
+            for (int k = 0; k < (TOTAL + C::THREADS - 1) / C::THREADS; ++k) {
+                const int c = k * C::THREADS + threadIdx.x;
+                if (TOTAL % C::THREADS != 0 && c >= TOTAL) break;
+                const int r = c / SO::CHUNKS, ch = c - r * SO::CHUNKS;
+                const int m = m0 + r, n = n0 + ch * (16 / (int)sizeof(T));
+                if (m < p.M && n < p.N)
+                    *reinterpret_cast<u32x4*>(y + (int64_t)m * p.ldy + n) =
+                        *reinterpret_cast<const u32x4*>(lds + r * SO::ROWE + ch * (16 / (int)sizeof(T)));
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int nb = 0; nb < C::NB; ++nb) {
         const int n = n0 + wn * C::WN + 16 * nb + 4 * (lane >> 4);
@@ -163,6 +214,7 @@ extern "C" int kf_proj_gemm(const void* x, const void* weight, const void* bias,
     p.K = (int)k;
     p.ldx = ldx;
     p.ldy = ldy;
+    p.staged_out = aligned(y, 16) && (ldy * es) % 16 == 0;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool b = bias != nullptr;
     if (dtype == KF_BF16) return launch_gemm_layout<bf16>(p, weight_layout, b, st);
