@@ -20,10 +20,16 @@ Head dim 32, bf16 or fp16.  The partials live in a workspace kept per
 (device, stream) and grown when a call needs more.
 
 ``prefer_fused`` is the modules' choice between this path and the unfused one
-(projection GEMM, then the linear-attention kernel): the fused tiles are tied
-to heads, so the fused path only wins once it has about three rounds of
-workgroups per CU (measured on MI355X: B=2, N=4096, C=2240 263 us fused vs
-269 us unfused; B=1, N=16384, C=1152 163 vs 174; B=1, N=1024, C=2240 85 vs 54).
+(projection GEMM, then the linear-attention kernel).  The fused tiles are tied
+to heads, so the fused path needs about three rounds of workgroups per CU;
+and where the projection's 3C output columns are a whole number of the
+GEMM's 224-wide tiles (heads a multiple of 7) the unfused GEMM loses nothing
+to a partial tile column and the fused path does not pay off.  Measured on
+MI355X (bf16, us, fused against unfused): B=2, N=8192 at 36 / 48 / 64 heads
+153 / 225 / 368 against 177 / 263 / 421; B=1, N=16384, 36 heads 157 against
+174; at 56 heads (B=2, N=8192) 342 against 334, at 70 heads (B=2, N=4096;
+B=1, N=16384) 260 / 504 against 258 / 486; B=1, N=4096, 70 heads 168 against
+145 (under two rounds).
 """
 
 from __future__ import annotations
@@ -60,10 +66,11 @@ def fused_applicable(dtype: torch.dtype, dim: int) -> bool:
 
 def prefer_fused(batch: int, seq_len: int, heads: int, device: torch.device) -> bool:
     """True when the fused path has at least three rounds of (token tile,
-    3-head group) workgroups per CU."""
+    3-head group) workgroups per CU and the unfused projection's output
+    columns (3 * 32 * heads) do not fill whole 224-wide GEMM tiles."""
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     tiles = batch * -(-seq_len // 256) * -(-heads // 3)
-    return tiles >= 3 * cus
+    return tiles >= 3 * cus and (3 * HEAD_DIM * heads) % 224 != 0
 
 
 def litela_fused_attention(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],

@@ -137,8 +137,11 @@ int launch_cfg(GemmParams p, bool bias, hipStream_t stream) {
 
 // Output-tile width for an M x N problem.  One workgroup runs per CU, so the
 // launch takes ceil(tiles / CUs) rounds, and a round costs about BN + 32
-// (work proportional to the width plus a fixed per-tile part; this model ranks
-// the measured times of every candidate correctly at the SANA shapes).
+// (work proportional to the width plus a fixed per-tile part), 5% more at
+// BN = 256, whose sub-tile is too large for the operand prefetch of the
+// mainloop (measured on MI355X: M = 16384, N = 6144, K = 2048 runs 377 us at
+// BN = 224 against 392 us at 256; N = 2048 still prefers 256, 124 against
+// 143 us).
 inline int pick_bn(int M, int N, const int* cands, int n_cands) {
     const int cus = device_cu_count();
     int best = cands[0];
@@ -146,7 +149,7 @@ inline int pick_bn(int M, int N, const int* cands, int n_cands) {
     for (int i = 0; i < n_cands; ++i) {
         const int bn = cands[i];
         const long long tiles = (long long)((M + 255) / 256) * ((N + bn - 1) / bn);
-        const long long cost = (tiles + cus - 1) / cus * (bn + 32);
+        const long long cost = (tiles + cus - 1) / cus * (bn + 32) * (bn == 256 ? 105 : 100);
         if (best_cost < 0 || cost < best_cost) {
             best_cost = cost;
             best = bn;
