@@ -293,9 +293,13 @@ __device__ __forceinline__ void gemm_mainloop(const GemmSrc<T>& src, WRow wrow, 
     auto xrow = [xr0, xlast](int r) { return min(xr0 + r, xlast); };
 
     // Scalar-base copies of whole stages when the tile's activation rows are
-    // all in range and its weight rows are linear in 8-row blocks.
+    // all in range, its weight rows are linear in 8-row blocks and a lane's
+    // offset within an instruction's rows fits the 32-bit offset operand.
     const int swave = __builtin_amdgcn_readfirstlane(wave);
-    const bool fast = !C::KN && src.w_rows_linear && xr0 + C::BM <= src.x_rows_end;
+    constexpr int64_t kMaxRowSpan = (int64_t)1 << 31;
+    const bool fast = !C::KN && src.w_rows_linear && xr0 + C::BM <= src.x_rows_end &&
+                      src.ldx * C::RPC * (int64_t)sizeof(T) < kMaxRowSpan &&
+                      (int64_t)src.K * C::RPC * (int64_t)sizeof(T) < kMaxRowSpan;
     const uint32_t x_voff = krows_lane_off<T, C>(src.ldx, swave, lane);
     const uint32_t w_voff = krows_lane_off<T, C>(src.K, swave, lane);
     const uint32_t lds0 = lds_addr(lds);
