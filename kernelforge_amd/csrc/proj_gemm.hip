@@ -92,9 +92,12 @@ void proj_gemm_kernel(GemmParams p) {
                 if (TOTAL % C::THREADS != 0 && c >= TOTAL) break;
                 const int r = c / SO::CHUNKS, ch = c - r * SO::CHUNKS;
                 const int m = m0 + r, n = n0 + ch * (16 / (int)sizeof(T));
+                // Nontemporal: 2.5-3.5% faster than plain stores at the
+                // config A shapes on MI355X (the output is not re-read here).
                 if (m < p.M && n < p.N)
-                    *reinterpret_cast<u32x4*>(y + (int64_t)m * p.ldy + n) =
-                        *reinterpret_cast<const u32x4*>(lds + r * SO::ROWE + ch * (16 / (int)sizeof(T)));
+                    __builtin_nontemporal_store(
+                        *reinterpret_cast<const u32x4*>(lds + r * SO::ROWE + ch * (16 / (int)sizeof(T))),
+                        reinterpret_cast<u32x4*>(y + (int64_t)m * p.ldy + n));
             }
             return;
         }
