@@ -21,15 +21,16 @@ Head dim 32, bf16 or fp16.  The partials live in a workspace kept per
 
 ``prefer_fused`` is the modules' choice between this path and the unfused one
 (projection GEMM, then the linear-attention kernel).  The fused tiles are tied
-to heads, so the fused path needs about three rounds of workgroups per CU;
-and where the projection's 3C output columns are a whole number of the
-GEMM's 224-wide tiles (heads a multiple of 7) the unfused GEMM loses nothing
-to a partial tile column and the fused path does not pay off.  Measured on
-MI355X (bf16, us, fused against unfused): B=2, N=8192 at 36 / 48 / 64 heads
-153 / 225 / 368 against 177 / 263 / 421; B=1, N=16384, 36 heads 157 against
-174; at 56 heads (B=2, N=8192) 342 against 334, at 70 heads (B=2, N=4096;
-B=1, N=16384) 260 / 504 against 258 / 486; B=1, N=4096, 70 heads 168 against
-145 (under two rounds).
+to heads, so the fused path needs about two rounds of workgroups per CU; and
+at head counts that are multiples of 7 (3C a whole number of the GEMM's 224-
+and, at 70 heads, 320-wide tiles) the unfused GEMM loses nothing to a partial
+tile column and the fused path does not pay off.  Measured on MI355X (bf16,
+us, fused against unfused): B=2, N=8192 at 36 / 48 / 64 heads 155 / 226 / 377
+against 175 / 271 / 410; B=1, N=16384, 36 heads 158 against 175; B=2,
+N=4096, 48 heads 132 against 153; but at 56 heads (B=2, N=8192; B=4, N=4096)
+351 / 350 against 344 / 344, at 70 heads (B=2, N=4096; B=1, N=16384; B=4,
+N=4096) 267 / 522 / 521 against 261 / 478 / 482, and under two rounds (B=2,
+N=4096, 36 heads) 105 against 101.
 """
 
 from __future__ import annotations
@@ -65,12 +66,13 @@ def fused_applicable(dtype: torch.dtype, dim: int) -> bool:
 
 
 def prefer_fused(batch: int, seq_len: int, heads: int, device: torch.device) -> bool:
-    """True when the fused path has at least three rounds of (token tile,
-    3-head group) workgroups per CU and the unfused projection's output
-    columns (3 * 32 * heads) do not fill whole 224-wide GEMM tiles."""
+    """True when the fused path has at least two rounds of (token tile,
+    3-head group) workgroups per CU and the head count is not a multiple of 7
+    (where the unfused projection's 3 * 32 * heads output columns fill whole
+    224-wide GEMM tiles)."""
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     tiles = batch * -(-seq_len // 256) * -(-heads // 3)
-    return tiles >= 3 * cus and (3 * HEAD_DIM * heads) % 224 != 0
+    return tiles >= 2 * cus and heads % 7 != 0
 
 
 def litela_fused_attention(x: torch.Tensor, qkv_weight: torch.Tensor, qkv_bias: Optional[torch.Tensor],

@@ -35,11 +35,15 @@ __device__ __forceinline__ void gemm_tile(int blk, int tiles_m, int tiles_n, int
 
 // Output tile staged in the (then free) stage buffers: rows of BN elements
 // plus 16 bytes, so the 16 rows one 8- or 16-byte staging write touches fall
-// on different banks.
+// on different banks.  A tile that does not fit goes through in PASSES bands
+// of whole wavefront rows (WM rows each).
 template <typename T, typename C> struct StagedOut {
     static constexpr int ROWE = C::BN + 16 / (int)sizeof(T);     // elements per staged row
     static constexpr int CHUNKS = C::BN * (int)sizeof(T) / 16;    // 16-byte chunks per output row
-    static constexpr bool FITS = C::BM * ROWE <= C::STAGES * (C::XS + C::WS);
+    static constexpr int SPACE = C::STAGES * (C::XS + C::WS);     // elements of the stage buffers
+    static constexpr int PASSES = C::BM * ROWE <= SPACE ? 1 : (C::BM / 2) * ROWE <= SPACE ? 2 : 4;
+    static constexpr int ROWS = C::BM / PASSES;                   // rows per pass
+    static constexpr bool FITS = ROWS * ROWE <= SPACE && ROWS % C::WM == 0;
 };
 
 template <typename T, typename C, bool BIAS>
@@ -66,38 +70,43 @@ void proj_gemm_kernel(GemmParams p) {
             // 16-byte chunks: full cache lines instead of the 32-byte row
             // pieces one MFMA block holds (which wrote 1.5x the output's
             // bytes at N = 2240).
-            __syncthreads();  // every wavefront is done with the stage buffers
 #pragma unroll
-            for (int nb = 0; nb < C::NB; ++nb) {
-                const int nl = wn * C::WN + 16 * nb + 4 * (lane >> 4);
-                float bv[4] = {0.f, 0.f, 0.f, 0.f};
-                if constexpr (BIAS) {
-                    if (n0 + nl < p.N) {
-                        const T* bias = static_cast<const T*>(p.bias) + n0 + nl;
+            for (int pass = 0; pass < SO::PASSES; ++pass) {
+                __syncthreads();  // the stage buffers (or the previous band) are free
+                if (wm * C::WM / SO::ROWS == pass) {
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) bv[i] = to_f32(bias[i]);
+                    for (int nb = 0; nb < C::NB; ++nb) {
+                        const int nl = wn * C::WN + 16 * nb + 4 * (lane >> 4);
+                        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+                        if constexpr (BIAS) {
+                            if (n0 + nl < p.N) {
+                                const T* bias = static_cast<const T*>(p.bias) + n0 + nl;
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) bv[i] = to_f32(bias[i]);
+                            }
+                        }
+#pragma unroll
+                        for (int mb = 0; mb < C::MB; ++mb) {
+                            const int ml = wm * C::WM - pass * SO::ROWS + 16 * mb + (lane & 15);
+                            store4(lds + ml * SO::ROWE + nl, acc[nb][mb], bv);
+                        }
                     }
                 }
+                __syncthreads();
+                constexpr int TOTAL = SO::ROWS * SO::CHUNKS;
 #pragma unroll
-                for (int mb = 0; mb < C::MB; ++mb) {
-                    const int ml = wm * C::WM + 16 * mb + (lane & 15);
-                    store4(lds + ml * SO::ROWE + nl, acc[nb][mb], bv);
+                for (int k = 0; k < (TOTAL + C::THREADS - 1) / C::THREADS; ++k) {
+                    const int c = k * C::THREADS + threadIdx.x;
+                    if (TOTAL % C::THREADS != 0 && c >= TOTAL) break;
+                    const int r = c / SO::CHUNKS, ch = c - r * SO::CHUNKS;
+                    const int m = m0 + pass * SO::ROWS + r, n = n0 + ch * (16 / (int)sizeof(T));
+                    // Nontemporal: 2.5-3.5% faster than plain stores at the
+                    // config A shapes on MI355X (the output is not re-read here).
+                    if (m < p.M && n < p.N)
+                        __builtin_nontemporal_store(
+                            *reinterpret_cast<const u32x4*>(lds + r * SO::ROWE + ch * (16 / (int)sizeof(T))),
+                            reinterpret_cast<u32x4*>(y + (int64_t)m * p.ldy + n));
                 }
-            }
-            __syncthreads();
-            constexpr int TOTAL = C::BM * SO::CHUNKS;
-#pragma unroll
-            for (int k = 0; k < (TOTAL + C::THREADS - 1) / C::THREADS; ++k) {
-                const int c = k * C::THREADS + threadIdx.x;
-                if (TOTAL % C::THREADS != 0 && c >= TOTAL) break;
-                const int r = c / SO::CHUNKS, ch = c - r * SO::CHUNKS;
-                const int m = m0 + r, n = n0 + ch * (16 / (int)sizeof(T));
-                // Nontemporal: 2.5-3.5% faster than plain stores at the
-                // config A shapes on MI355X (the output is not re-read here).
-                if (m < p.M && n < p.N)
-                    __builtin_nontemporal_store(
-                        *reinterpret_cast<const u32x4*>(lds + r * SO::ROWE + ch * (16 / (int)sizeof(T))),
-                        reinterpret_cast<u32x4*>(y + (int64_t)m * p.ldy + n));
             }
             return;
         }
@@ -139,12 +148,12 @@ int launch_cfg(GemmParams p, bool bias, hipStream_t stream) {
 }
 
 // Output-tile width for an M x N problem.  One workgroup runs per CU, so the
-// launch takes ceil(tiles / CUs) rounds, and a round costs about BN + 32
-// (work proportional to the width plus a fixed per-tile part), 5% more at
-// BN = 256, whose sub-tile is too large for the operand prefetch of the
-// mainloop (measured on MI355X: M = 16384, N = 6144, K = 2048 runs 377 us at
-// BN = 224 against 392 us at 256; N = 2048 still prefers 256, 124 against
-// 143 us).
+// launch takes ceil(tiles / CUs) rounds, and a round of BN-wide tiles costs
+// about BN + 92 (a fixed per-tile part plus work proportional to the width).
+// Fitted to a sweep of every width over nine shapes on MI355X (M = 4096-16384,
+// N = 1152-6720, K = 1152-2240): per round at K = 2240 about 36 us at BN = 128,
+// 42 at 160, 47 at 192, 54 at 224, 56-62 at 256 and 66-72 at 320; the model
+// picks the fastest width, or one within 1.5% of it, at all nine.
 inline int pick_bn(int M, int N, const int* cands, int n_cands) {
     const int cus = device_cu_count();
     int best = cands[0];
@@ -152,7 +161,7 @@ inline int pick_bn(int M, int N, const int* cands, int n_cands) {
     for (int i = 0; i < n_cands; ++i) {
         const int bn = cands[i];
         const long long tiles = (long long)((M + 255) / 256) * ((N + bn - 1) / bn);
-        const long long cost = (tiles + cus - 1) / cus * (bn + 32) * (bn == 256 ? 105 : 100);
+        const long long cost = (tiles + cus - 1) / cus * (bn + 92);
         if (best_cost < 0 || cost < best_cost) {
             best_cost = cost;
             best = bn;
@@ -163,10 +172,11 @@ inline int pick_bn(int M, int N, const int* cands, int n_cands) {
 
 template <typename T, bool KN>
 int launch_gemm(const GemmParams& p, bool bias, hipStream_t st) {
-    // 16-bit weights in [N][K]: five widths; fp32 or WeightT: 256 and 128.
+    // 16-bit weights in [N][K]: six widths; fp32 or WeightT: 256 and 128.
     if constexpr (sizeof(T) == 2 && !KN) {
-        static const int cands[] = {224, 256, 192, 160, 128};
-        switch (pick_bn(p.M, p.N, cands, 5)) {
+        static const int cands[] = {320, 224, 256, 192, 160, 128};
+        switch (pick_bn(p.M, p.N, cands, 6)) {
+        case 320: return launch_cfg<typename ProjTile<T, 320, KN>::C>(p, bias, st);
         case 256: return launch_cfg<typename ProjTile<T, 256, KN>::C>(p, bias, st);
         case 224: return launch_cfg<typename ProjTile<T, 224, KN>::C>(p, bias, st);
         case 192: return launch_cfg<typename ProjTile<T, 192, KN>::C>(p, bias, st);

@@ -74,12 +74,14 @@ def test_integer_inputs_round_once_bit_exact(dtype, layout, bias):
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16))
 def test_every_tile_width(dtype):
-    """The launch picks the output-tile width (256, 224, 192, 160 or 128
+    """The launch picks the output-tile width (320, 256, 224, 192, 160 or 128
     channels) from the shape; on a 256-CU MI355X these shapes select each of
-    them (16384x2048 -> 256, 8192x6720 -> 224, 8192x1536 -> 192,
-    8192x2240 -> 160, 300x264 -> 128).  K = 72 adds a one-chunk K tail."""
+    them (8192x6720 -> 320, 16384x2048 -> 256, 4096x6720 -> 224,
+    8192x1536 -> 192, 2048x4480 -> 160, 300x264 -> 128; 320 and 256 store the
+    output tile in two row bands).  K = 72 adds a one-chunk K tail."""
     K = 72
-    for i, (M, N) in enumerate(((16384, 2048), (8192, 6720), (8192, 1536), (8192, 2240), (300, 264))):
+    shapes = ((8192, 6720), (16384, 2048), (4096, 6720), (8192, 1536), (2048, 4480), (300, 264))
+    for i, (M, N) in enumerate(shapes):
         print(f"proj width case dtype={dtype} M={M} N={N} K={K}", flush=True)
         x = _ints((M, K), -3, 3, 40 + i, dtype)
         w = _ints((N, K), -3, 3, 50 + i, dtype)
