@@ -91,6 +91,31 @@ def test_every_tile_width(dtype):
 
 
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
+@pytest.mark.parametrize("layout", ("nk", "kn"))
+def test_wide_tiles_ragged_and_banded(dtype, layout):
+    """The wide tiles (320 and 256 channels) store their output through LDS in
+    two (fp32: four) row bands; these shapes select them with a partial last
+    row tile and a partial last column tile (16-bit nn.Linear layout:
+    7999x2216 -> 320, 8000x1992 -> 256; fp32 or WeightT: 16000x2040 -> 256)."""
+    K = 72
+    if dtype != torch.float32 and layout == "nk":
+        shapes = ((7999, 2216), (8000, 1992))
+    else:
+        shapes = ((16000, 2040),)
+    for i, (M, N) in enumerate(shapes):
+        print(f"proj wide case dtype={dtype} layout={layout} M={M} N={N} K={K}", flush=True)
+        x = _ints((M, K), -3, 3, 70 + i, dtype)
+        w = _ints((N, K), -3, 3, 80 + i, dtype)
+        b = _ints((N,), -50, 50, 90 + i, dtype)
+        xd, bd = x.to(DEV), b.to(DEV)
+        if layout == "nk":
+            y = linear(xd, w.to(DEV), bd)
+        else:
+            y = linear_t(xd, w.T.contiguous().to(DEV), bd)
+        assert torch.equal(y.cpu(), _ref64(x, w, b).to(dtype)), (M, N)
+
+
+@pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
 def test_random_inputs_within_the_accumulation_bound(dtype):
     for M, N, K in ((1024, 6720, 2240), (333, 2240, 2240), (64, 3456, 1152)):
         print(f"proj random case dtype={dtype} M={M} N={N} K={K}", flush=True)
