@@ -16,10 +16,10 @@
 // staging), STAGES buffers deep.  Copies of whole stages of in-range rows take
 // a scalar base per instruction and one per-lane offset per wavefront, so
 // they cost no vector instructions; others compute a clamped address per lane.
-// Each wavefront owns a WM x WN sub-tile.  A
-// lane reads one 16-byte chunk per operand block and 64-byte K step: one
-// v_mfma_f32_16x16x32 for bf16/f16, four v_mfma_f32_16x16x4f32 for fp32, whose
-// K slices are taken as {4g + t} so that the same chunk read serves all four.
+// Each wavefront owns a WM x WN sub-tile.  A lane reads one 16-byte chunk per
+// operand block and 64-byte K step: one v_mfma_f32_16x16x32 for bf16/f16,
+// four v_mfma_f32_16x16x4f32 for fp32, whose K slices are taken as {4g + t}
+// so that the same chunk read serves all four.
 // The MFMA computes the transposed product (A = weight rows, B = activation
 // rows), so a lane ends with 4 consecutive output channels of one token.
 //
