@@ -133,6 +133,26 @@ def test_random_inputs_within_the_accumulation_bound(dtype):
         assert bool(((dropped - y64).abs() > bound).any())
 
 
+@pytest.mark.parametrize("n_out,bias", ((6720, False), (2240, True)))
+def test_config_a_random_rows_within_the_accumulation_bound(n_out, bias):
+    """Both config-A projections (x [8192, 2240] bf16, 320-wide tiles) on
+    random inputs: 64 rows spread over every row tile, all columns, against
+    the fp64 product and the accumulation bound."""
+    M, K = 8192, 2240
+    dtype = torch.bfloat16
+    print(f"proj config A random rows N={n_out} bias={bias}", flush=True)
+    g = torch.Generator().manual_seed(n_out)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(n_out, K, generator=g) / K ** 0.5).to(dtype)
+    b = torch.randn(n_out, generator=g).to(dtype) if bias else None
+    y = linear(x.to(DEV), w.to(DEV), b.to(DEV) if bias else None).cpu().double()
+    rows = torch.randperm(M, generator=g)[:64]
+    y64 = _ref64(x[rows], w, b)
+    err = (y[rows] - y64).abs()
+    bound = _bound(x[rows], w, y64, dtype)
+    assert bool((err <= bound).all()), float((err - bound).max())
+
+
 @pytest.mark.parametrize("dtype", (torch.bfloat16, torch.float16, torch.float32))
 def test_weight_layouts_agree_bitwise(dtype):
     """The [N, K] and the prepacked [K, N] weight feed the same operands to the
