@@ -165,11 +165,14 @@ def test_weight_layouts_agree_bitwise(dtype):
     assert torch.equal(linear(x, w, b), linear_t(x, w.T.contiguous(), b))
 
 
-def test_strided_rows_and_untouched_padding():
+@pytest.mark.parametrize("ldy_pad", (12, 8))
+def test_strided_rows_and_untouched_padding(ldy_pad):
     """ldx > K with NaN padding beyond K (never read) and ldy > N (padding
-    columns never written), through the C ABI."""
+    columns never written), through the C ABI.  A row stride of 8 extra
+    elements keeps output rows 16-byte aligned (the LDS-staged output path),
+    12 does not (per-lane stores)."""
     lib = _lib.load()
-    M, N, K, ldx, ldy = 300, 264, 520, 520 + 24, 264 + 12
+    M, N, K, ldx, ldy = 300, 264, 520, 520 + 24, 264 + ldy_pad
     x = _ints((M, ldx), -3, 3, 1, torch.bfloat16)
     x[:, K:] = float("nan")
     w = _ints((N, K), -3, 3, 2, torch.bfloat16)
