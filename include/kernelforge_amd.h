@@ -357,9 +357,12 @@ int kf_fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
  * tO from the cached LSE (standalone JVP, no forward launch):
  *   P = exp(scale*q k^T - lse),  tS = scale*(tq k^T + q tk^T),  H = P*tS,
  *   tO = P tv + H v - rowsum(H) * O.
- * O is recomputed in fp32 from the same P inside the kernel (U = P v): the
- * cached 16-bit `o` is accepted for interface parity and is not read,
- * because rowsum(H) would amplify its rounding error.
+ * O is the cached `o`, as in the reference, while |rowsum(H)/l| * max(max|O|,
+ * 1) <= 1 on every row of a 128-row tile (l = rowsum of the 16-bit P); a tile
+ * past that bound, where rowsum(H) could amplify o's rounding beyond about a
+ * fifth of the bf16 tolerance, is redone by a second launch that recomputes
+ * O in fp32 from the same P (U = P v) and does not read `o`.  Two launches,
+ * the second exits at once for tiles under the bound.
  * Any of tq, tk, tv may be NULL, meaning a zero tangent.
  * Replaces kernelforge::flash_attention_jvp / _attention_jvp_kernel
  * (flash_attention_jvp/custom.py:12-120, 137-152).

@@ -67,6 +67,13 @@ template <int DP> struct FaTile {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleThreshold = 8.0f;  // lazy rescale step of the rescaling scan (log2)
+// The JVP-from-LSE mode writes tO = G/l - (r/l) O with the cached O only for
+// rows where |r/l| * max(max|O|, 1) is at most this: O's rounding (a few
+// 2^-9 relative) then moves tO by at most ~2^-8 of it, about a fifth of the
+// 2e-2 tolerance (a CPU emulation of every rounding point over D = 32-128,
+// N = 64-2048 and scales 0.05-1.3 measured at most 0.24 of it).  At scale
+// 1/sqrt(D) on unit-normal inputs the product stays below ~0.6.
+constexpr float kCachedOBound = 1.0f;
 
 // 256 bytes of zeros in global memory: the source of lanes whose chunk is
 // outside the tensor (key rows >= Nk, head-dim padding).

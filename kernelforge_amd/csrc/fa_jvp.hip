@@ -7,11 +7,17 @@
 //   l = sum E, U = E v, r = sum E*tS, G = (E*tS) v + E tv;
 //   O = U/l, tO = G/l - (r/l) O, LSE = m + log l.
 // The JVP-from-LSE mode recomputes P = exp(S - LSE) (flash_attention_jvp/
-// custom.py:88-118) and, unlike the reference, does not use the cached 16-bit
-// O in tO = P tv + H v - rowsum(H) O: that term multiplies O's rounding error
-// by rowsum(H), which exceeds the bf16 tolerance at D = 128.  It accumulates
-// U = P v alongside (one more product) and normalises like the fused mode:
-//   tO = (P tv + H v)/l - (rowsum(H)/l) (U/l),  l = rowsum(P) of the rounded P.
+// custom.py:88-118) and, like the reference, takes O from the cached 16-bit
+// output, five products per key tile:
+//   tO = (P tv + H v)/l - (rowsum(H)/l) O,  l = rowsum(P) of the rounded P.
+// The second term multiplies O's rounding error (2^-9 relative, plus the
+// forward's own rounding of P) by rowsum(H)/l, which a peaked softmax makes
+// large enough to break the bf16 tolerance.  So a row is written this way
+// only while |rowsum(H)/l| * max(max|O|, 1) <= kCachedOBound; otherwise its
+// workgroup redoes all its rows in a second scan that also accumulates
+// U = P v (a sixth product) and uses U/l, which carries exactly the rounding
+// of the P in the other terms:
+//   tO = (P tv + H v)/l - (rowsum(H)/l) (U/l).
 //
 // Tiling.  A workgroup is 8 wavefronts x 16 query rows (128 rows) of one
 // (batch, head), two wavefronts per SIMD so that one wavefront's softmax
@@ -82,13 +88,17 @@ template <int DP, int MODE> constexpr int fa_rows() { return FaTile<DP>::BQ * fa
 // state; the workgroup then writes NaN into the LSE of its rows (and nothing
 // else), and fa_fixup_kernel redoes those rows with LAZY = true, which raises
 // the reference whenever a half's max exceeds it by 2^3 and rescales the
-// state.  kbuf0/1 and vbuf0/1 are the two K-side and V-side LDS buffers, NT
-// tiles each.
+// state.  In the JVP-from-LSE mode LAZY = false is the cached-O scan (five
+// products): a workgroup with a row past kCachedOBound writes NaN into the
+// first tO element of its rows (and nothing else), and fa_fixup_kernel redoes
+// those rows with LAZY = true, the scan that recomputes U.  kbuf0/1 and
+// vbuf0/1 are the two K-side and V-side LDS buffers, NT tiles each.
 template <typename T, int DP, int MODE, bool ALL, bool LAZY>
 __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T* vbuf0, T* vbuf1) {
     constexpr int R = fa_row_blocks<DP, MODE>();
     constexpr int kBQ = fa_rows<DP, MODE>(), kBK = FaTile<DP>::BK;
     constexpr bool JVP = MODE != FA_FWD;
+    constexpr bool kCachedO = MODE == FA_JVP && !LAZY;  // O from p.o, no U products
     constexpr int NT = JVP ? 2 : 1;   // tensors per side: K (, tK) and V (, tV)
     constexpr int DS = DP / 32;        // 32-wide K-steps of the score products
     constexpr int DB = DP / 16;        // 16-wide d blocks of the outputs
@@ -157,6 +167,24 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
                 tqreg[rb][ds] = __builtin_bit_cast(x8, t);
             }
         }
+    // The cached O values this lane's output elements need (d = 16*db +
+    // 4*grp + 0..3; D % 8 == 0, so a chunk below D lies wholly below it).
+    typename V<T>::x4 ocv[R][kCachedO ? DB : 1];
+    if constexpr (kCachedO) {
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb)
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const int d = 16 * db + 4 * grp;
+                typename V<T>::x4 z;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) z[e] = (T)0.f;
+                ocv[rb][db] = row_ok[rb] && d < p.D
+                                  ? *reinterpret_cast<const typename V<T>::x4*>(static_cast<const T*>(p.o) +
+                                                                                 q_off[rb] + d)
+                                  : z;
+            }
+    }
 
     // Key range of the workgroup.
     int key_stop = p.Nk;
@@ -370,7 +398,8 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
             g[rb][db] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
-    // O^T += V^T E^T ; G^T += V^T H^T + tV^T E^T over the 32 keys of half h
+    // O^T += V^T E^T (not in the cached-O scan) ; G^T += V^T H^T + tV^T E^T
+    // over the 32 keys of half h
     // of the tile in buffer bufc.
     auto pv = [&](auto bufc, int h, const u32x2 (&ew)[R][2], const u32x2 (&hw)[R][2]) {
         x8 eb[R], hb[R];
@@ -413,7 +442,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
                 const x8 va = vring[db % NR];
 #pragma unroll
                 for (int rb = 0; rb < R; ++rb) {
-                    u[rb][db] = mfma16x16x32(va, eb[rb], u[rb][db]);
+                    if constexpr (!kCachedO) u[rb][db] = mfma16x16x32(va, eb[rb], u[rb][db]);
                     if constexpr (JVP) {
                         g[rb][db] = mfma16x16x32(va, hb[rb], g[rb][db]);
                         if (use_tv) g[rb][db] = mfma16x16x32(tvring[db % NR], eb[rb], g[rb][db]);
@@ -521,6 +550,51 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
         }
     }
 
+    if constexpr (kCachedO) {
+        // tO = G/l - (r/l) O with the cached O, unless a row's r/l could
+        // amplify O's rounding past the bound: then only the markers are
+        // written and fa_fixup_kernel redoes the workgroup's rows with U
+        // (uniform over the workgroup: that scan needs every wavefront for its
+        // tile copies).
+        float inv[R], rl[R];
+        bool over = false;
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            const float l_tot = row_sum4(l_run[rb]);
+            inv[rb] = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            rl[rb] = row_sum4(r_run[rb]) * inv[rb];
+            float om = 0.f;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) om = fmaxf(om, fabsf((float)ocv[rb][db][e]));
+            om = row_max4(om);
+            over = over || (row_ok[rb] && fabsf(rl[rb]) * fmaxf(om, 1.f) > kCachedOBound);
+        }
+        if (__syncthreads_or(over)) {
+#pragma unroll
+            for (int rb = 0; rb < R; ++rb)
+                if (grp == 0 && row_ok[rb]) static_cast<T*>(p.to)[q_off[rb]] = (T)__builtin_nanf("");
+            return;
+        }
+#pragma unroll
+        for (int rb = 0; rb < R; ++rb) {
+            T* torow = static_cast<T*>(p.to) + q_off[rb];
+#pragma unroll
+            for (int db = 0; db < DB; ++db) {
+                const int d = 16 * db + 4 * grp;
+                if (row_ok[rb] && d < p.D) {
+                    typename V<T>::x4 tv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        tv[e] = (T)(g[rb][db][e] * inv[rb] - rl[rb] * (float)ocv[rb][db][e]);
+                    *reinterpret_cast<typename V<T>::x4*>(torow + d) = tv;
+                }
+            }
+        }
+        return;
+    }
+
     // ---- epilogue: O = U/l, tO = G/l - (r/l) O, LSE = m + log l ----
 #pragma unroll
     for (int rb = 0; rb < R; ++rb) {
@@ -573,10 +647,12 @@ void fa_kernel(const FaParams p) {
     fa_scan<T, DP, MODE, ALL, false>(p, kside0, kside1, vside0, vside1);
 }
 
-// Second launch of the FWD/FWD_JVP modes: a workgroup whose rows carry the
-// overflow marker (NaN LSE) redoes them with the rescaling scan; every other
-// workgroup reads its LSE entries and exits.  A separate kernel keeps the
-// rescaling code out of the fast scan's register allocation.
+// Second launch of every mode: a workgroup whose rows carry the marker redoes
+// them with the LAZY = true scan (the rescaling scan in FWD/FWD_JVP, marker NaN
+// LSE; the scan that recomputes U in the JVP-from-LSE mode, marker NaN in the
+// first tO element); every other workgroup reads its markers and exits.  A
+// separate kernel keeps that code out of the fast scan's register allocation
+// (inlined, the two scans spill at D = 128).
 template <typename T, int DP, int MODE, bool ALL>
 __global__ __launch_bounds__(FaTile<DP>::THREADS)
 __attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
@@ -586,8 +662,13 @@ void fa_fixup_kernel(const FaParams p) {
     static_assert(kBQ <= FaTile<DP>::THREADS, "one thread per row checks the marker");
     const int row = blk.qtile * kBQ + (int)threadIdx.x;
     bool marked = false;
-    if (threadIdx.x < kBQ && row < p.Nq)
-        marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
+    if (threadIdx.x < kBQ && row < p.Nq) {
+        if constexpr (MODE == FA_JVP)
+            marked = __builtin_isnan(
+                (float)static_cast<const T*>(p.to)[((int64_t)blk.b * p.Nq + row) * p.Hq * p.D + (int64_t)blk.hq * p.D]);
+        else
+            marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
+    }
     if (!__syncthreads_or(marked)) return;
     FA_LDS_BUFFERS(T, DP, MODE);
     fa_scan<T, DP, MODE, ALL, true>(p, kside0, kside1, vside0, vside1);
@@ -604,13 +685,10 @@ int launch_variant(const FaParams& p, int dp, hipStream_t stream) {
     auto launch = [&](auto dpc) {
         constexpr int DP = decltype(dpc)::value;
         hipLaunchKernelGGL((fa_kernel<T, DP, MODE, ALL>), grid, dim3(FaTile<DP>::THREADS), 0, stream, p);
-        if constexpr (MODE != FA_JVP) {
-            const int rc = check_launch("fa_kernel launch");
-            if (rc != KF_OK) return rc;
-            hipLaunchKernelGGL((fa_fixup_kernel<T, DP, MODE, ALL>), grid, dim3(FaTile<DP>::THREADS), 0, stream, p);
-            return check_launch("fa_fixup_kernel launch");
-        }
-        return check_launch("fa_kernel launch");
+        const int rc = check_launch("fa_kernel launch");
+        if (rc != KF_OK) return rc;
+        hipLaunchKernelGGL((fa_fixup_kernel<T, DP, MODE, ALL>), grid, dim3(FaTile<DP>::THREADS), 0, stream, p);
+        return check_launch("fa_fixup_kernel launch");
     };
     switch (dp) {
         case 32: return launch(std::integral_constant<int, 32>{});

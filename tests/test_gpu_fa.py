@@ -187,6 +187,41 @@ def test_absent_tangents(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_jvp_reads_the_cached_output(dtype):
+    """At scale 1/sqrt(D) the standalone JVP takes O from `out`, as the
+    reference's kernel does: a shifted `out` moves tO by -rowsum(H) * shift,
+    and the result follows the reference's dense formula for that `out`."""
+    case = (1, 200, 300, 2, 2, 64, False, None)
+    q, k, v, tq, tk, tv = seeded(case, dtype)
+    out, lse = flash_attention(q, k, v, return_lse=True)
+    shifted = (out.float() + 0.125).to(dtype)
+    plain = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse)
+    moved = flash_attention_jvp(q, k, v, tq, tk, tv, shifted, lse)
+    assert not torch.equal(plain, moved)
+    for cached, tangent in ((out, plain), (shifted, moved)):
+        dense = orc.attention_jvp_from_forward(*(t.cpu() for t in (q, k, v, tq, tk, tv, cached, lse)))
+        torch.testing.assert_close(tangent.cpu(), dense, **BOUNDS[dtype])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_jvp_peaked_rows_recompute_the_output(dtype):
+    """With scale 1 at D = 32 most rows' rowsum(H)/l would amplify the cached
+    O's rounding past the kernel's bound, so their tiles are redone with O
+    recomputed from the same probabilities: tO no longer depends on `out` and
+    stays within the tolerance of the fp64 oracle (the reference's formula
+    with the cached O does not, on such rows)."""
+    case = (2, 64, 80, 2, 2, 32, False, 1.0)
+    q, k, v, tq, tk, tv = seeded(case, dtype)
+    out, lse = flash_attention(q, k, v, return_lse=True, softmax_scale=1.0)
+    nudged = (out.float() * (1 + 2 ** -6)).to(dtype)
+    first = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, softmax_scale=1.0)
+    second = flash_attention_jvp(q, k, v, tq, tk, tv, nudged, lse, softmax_scale=1.0)
+    assert torch.equal(first, second)
+    _, expected = orc.attention_jvp(*on_cpu64((q, k, v, tq, tk, tv)), softmax_scale=1.0)
+    close(first, expected, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_uniform_score_shift_and_schedule_arguments(dtype):
     """A key tangent with q.tk the same for every key shifts all scores of a row
     by one constant: the softmax, hence O, does not move and tO = 0.  Explicit
