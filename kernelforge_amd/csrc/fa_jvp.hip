@@ -90,8 +90,8 @@ template <int DP, int MODE> constexpr int fa_rows() { return FaTile<DP>::BQ * fa
 // the reference whenever a half's max exceeds it by 2^3 and rescales the
 // state.  In the JVP-from-LSE mode LAZY = false is the cached-O scan (five
 // products): a workgroup with a row past kCachedOBound writes NaN into the
-// first tO element of its rows (and nothing else), and fa_fixup_kernel redoes
-// those rows with LAZY = true, the scan that recomputes U.  kbuf0/1 and
+// first tO element of its first row (and nothing else), and fa_fixup_kernel
+// redoes its rows with LAZY = true, the scan that recomputes U.  kbuf0/1 and
 // vbuf0/1 are the two K-side and V-side LDS buffers, NT tiles each.
 template <typename T, int DP, int MODE, bool ALL, bool LAZY>
 __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T* vbuf0, T* vbuf1) {
@@ -552,7 +552,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
 
     if constexpr (kCachedO) {
         // tO = G/l - (r/l) O with the cached O, unless a row's r/l could
-        // amplify O's rounding past the bound: then only the markers are
+        // amplify O's rounding past the bound: then only the marker is
         // written and fa_fixup_kernel redoes the workgroup's rows with U
         // (uniform over the workgroup: that scan needs every wavefront for its
         // tile copies).
@@ -572,9 +572,9 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
             over = over || (row_ok[rb] && fabsf(rl[rb]) * fmaxf(om, 1.f) > kCachedOBound);
         }
         if (__syncthreads_or(over)) {
-#pragma unroll
-            for (int rb = 0; rb < R; ++rb)
-                if (grp == 0 && row_ok[rb]) static_cast<T*>(p.to)[q_off[rb]] = (T)__builtin_nanf("");
+            // The marker: NaN in the first element of the workgroup's first
+            // row (wavefront 0, lane 0; that row always exists).
+            if (wave == 0 && lane == 0) static_cast<T*>(p.to)[q_off[0]] = (T)__builtin_nanf("");
             return;
         }
 #pragma unroll
@@ -650,9 +650,9 @@ void fa_kernel(const FaParams p) {
 // Second launch of every mode: a workgroup whose rows carry the marker redoes
 // them with the LAZY = true scan (the rescaling scan in FWD/FWD_JVP, marker NaN
 // LSE; the scan that recomputes U in the JVP-from-LSE mode, marker NaN in the
-// first tO element); every other workgroup reads its markers and exits.  A
-// separate kernel keeps that code out of the fast scan's register allocation
-// (inlined, the two scans spill at D = 128).
+// first tO element of the workgroup's first row); every other workgroup reads
+// its markers and exits.  A separate kernel keeps that code out of the fast
+// scan's register allocation (inlined, the two scans spill at D = 128).
 template <typename T, int DP, int MODE, bool ALL>
 __global__ __launch_bounds__(FaTile<DP>::THREADS)
 __attribute__((amdgpu_waves_per_eu(FaTile<DP>::OCC, FaTile<DP>::OCC)))
@@ -662,12 +662,12 @@ void fa_fixup_kernel(const FaParams p) {
     static_assert(kBQ <= FaTile<DP>::THREADS, "one thread per row checks the marker");
     const int row = blk.qtile * kBQ + (int)threadIdx.x;
     bool marked = false;
-    if (threadIdx.x < kBQ && row < p.Nq) {
-        if constexpr (MODE == FA_JVP)
+    if constexpr (MODE == FA_JVP) {
+        if (threadIdx.x == 0)
             marked = __builtin_isnan(
                 (float)static_cast<const T*>(p.to)[((int64_t)blk.b * p.Nq + row) * p.Hq * p.D + (int64_t)blk.hq * p.D]);
-        else
-            marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
+    } else if (threadIdx.x < kBQ && row < p.Nq) {
+        marked = __builtin_isnan(p.lse[((int64_t)blk.b * p.Hq + blk.hq) * p.Nq + row]);
     }
     if (!__syncthreads_or(marked)) return;
     FA_LDS_BUFFERS(T, DP, MODE);
