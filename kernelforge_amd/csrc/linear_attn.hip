@@ -121,6 +121,7 @@ struct FusedParams {
     int N, H, npairs, S, split_len;
     int g0;             // first group (batch * npairs + pair) of this launch
     int total;          // workgroups of this launch: groups * S
+    int use_ticket;     // 1: number workgroups by ticket (more than the device holds at once)
     int spin_limit;     // polls of a group counter before a member gives up
     float eps;
 };
@@ -222,16 +223,22 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
 
 // --------------------------------------------------------------------------
 // The fused kernel (D = 32, 16-bit input).  One workgroup per (batch, head
-// pair, sequence split), numbered by a ticket taken at start, so the members
-// of a group start consecutively: a member can only wait for members that
-// started before it or will start next, and at most one group is partly
-// started at any time.  Workgroups of fully started groups wait for nobody
-// who has not started, so they finish and free their slots; the partly
-// started group's waiting members hold at most S - 1 slots, and the host
-// keeps S within the slots the device offers (invariant 3 below), so its
-// remaining members always find a slot and every wait ends.  Only other
-// work holding the device's slots for longer than the poll limit can make a
-// member give up (then it reports it: see group_barrier).
+// pair, sequence split).  A launch whose workgroups all fit on the device at
+// once (the default split counts keep it so) numbers them by workgroup
+// index: every member a waiting workgroup needs then holds a slot or gets
+// one, whatever order the hardware starts them in.  A larger launch numbers
+// them by a ticket taken at start, so the members of a group start
+// consecutively: a member can only wait for members that started before it
+// or will start next, and at most one group is partly started at any time.
+// Workgroups of fully started groups wait for nobody who has not started, so
+// they finish and free their slots; the partly started group's waiting
+// members hold at most S - 1 slots, and the host keeps S within the slots the
+// device offers (invariant 3 below), so its remaining members always find a
+// slot and every wait ends.  (The ticket is one atomic counter for the whole
+// launch: 210 workgroups taking it cost ~2 us at B=2, H=70, N=4096 on MI355X,
+// so the smaller launches skip it.)  Only other work holding the device's
+// slots for longer than the poll limit can make a member give up (then it
+// reports it: see group_barrier).
 //   Phase 1: stream the split's K and V (three 128-token tiles in flight in
 //            registers, LDS double buffer), accumulate the partial state
 //            S = V^T relu(K) with v_mfma_f32_32x32x16 and z = sum relu(K),
@@ -280,18 +287,21 @@ __global__ __launch_bounds__(kThreads) void linattn_fused_kernel(FusedParams p) 
     __shared__ int sh_late;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) {
-        const int t = (int)__hip_atomic_fetch_add(p.ctrl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (t == p.total - 1) __hip_atomic_store(p.ctrl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sh_ticket = t;
-    }
-    __syncthreads();
-    const int ticket = sh_ticket;
-    if (ticket >= p.total) {
-        // Control words that were not zero on entry: flag it and touch nothing
-        // (the group barriers of the other workgroups then time out).
-        if (tid == 0) __hip_atomic_store(p.ctrl + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+    int ticket = blockIdx.x;
+    if (p.use_ticket) {
+        if (tid == 0) {
+            const int t = (int)__hip_atomic_fetch_add(p.ctrl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (t == p.total - 1) __hip_atomic_store(p.ctrl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sh_ticket = t;
+        }
+        __syncthreads();
+        ticket = sh_ticket;
+        if (ticket >= p.total) {
+            // Control words that were not zero on entry: flag it and touch
+            // nothing (the group barriers of the other workgroups then time out).
+            if (tid == 0) __hip_atomic_store(p.ctrl + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
     }
     const int g = ticket / p.S, s = ticket - g * p.S;  // group within this launch, split
     const int gg = p.g0 + g;
@@ -808,6 +818,7 @@ struct Launch {
     int B, N, H, D, S, L;  // S splits of L tokens
     float eps;
     int spin_limit;
+    bool force_ticket;     // number workgroups by ticket even when all fit at once
     bool out_tn;           // out[b][c][t] instead of out[b][t][c]
     hipStream_t stream;
 };
@@ -861,6 +872,7 @@ int run_mfma(const Launch& a) {
     p.spin_limit = a.spin_limit;
     p.eps = a.eps;
     const int64_t groups = (int64_t)a.B * p.npairs;
+    const int64_t slots = fused_slots<T, TO, OT>();
     // Groups per launch: the control region holds kMaxGroupsPerLaunch groups,
     // and a launch's workgroup count stays below 2^31.
     int64_t per = kMaxGroupsPerLaunch;
@@ -869,6 +881,7 @@ int run_mfma(const Launch& a) {
         const int64_t n = groups - g0 < per ? groups - g0 : per;
         p.g0 = (int)g0;
         p.total = (int)(n * a.S);
+        p.use_ticket = p.total > slots || a.force_ticket ? 1 : 0;
         hipLaunchKernelGGL((linattn_fused_kernel<T, TO, OT>), dim3((unsigned)p.total), dim3(kThreads), 0, a.stream,
                            p);
         if (int rc = check_launch("linattn_fused_kernel launch")) return rc;
@@ -976,7 +989,7 @@ int zero_words(void* ws, int64_t bytes, hipStream_t s) {
 // words, the partials and (generic path) the reduced states.
 int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_bytes, int64_t batch,
                 int64_t seq_len, int64_t heads, int64_t dim, int64_t splits, float eps, int in_dtype,
-                int out_dtype, bool out_tn, int spin_limit, hipStream_t s) {
+                int out_dtype, bool out_tn, int spin_limit, hipStream_t s, bool force_ticket = false) {
     KF_REQUIRE(qkv && out, KF_E_INVALID, "linattn: null pointer");
     int64_t split_len = 0;
     const int64_t eff = resolve_splits(batch, seq_len, heads, dim, splits, in_dtype, out_dtype, out_tn, &split_len);
@@ -1007,6 +1020,7 @@ int linattn_run(const void* qkv, void* out, void* workspace, int64_t workspace_b
     a.ws.state = a.ws.partial + batch * heads * (dim + 1) * dim * a.S;
     a.eps = eps;
     a.spin_limit = spin_limit;
+    a.force_ticket = force_ticket;
     a.out_tn = out_tn;
     a.stream = s;
     switch (in_dtype) {
@@ -1173,8 +1187,9 @@ extern "C" int kf_linattn_noalloc_check(kf_stream_t stream) {
 //
 // kf_linattn_fwd with the number of polls a member of the fused kernel makes
 // at its group's counter before giving up (and writing NaN); polls <= 0 or
-// above the default take the default.  Lets a test drive the give-up path
-// from the host without any global state.
+// above the default take the default.  A cut limit also selects ticket
+// numbering.  Lets a test drive the give-up path from the host without any
+// global state.
 extern "C" int kfm_linattn_fwd_spin(const void* qkv, void* out, void* workspace, int64_t workspace_bytes,
                                     int64_t batch, int64_t seq_len, int64_t heads, int64_t dim, int64_t splits,
                                     float eps, int in_dtype, int out_dtype, int64_t polls, kf_stream_t stream) {
@@ -1182,8 +1197,11 @@ extern "C" int kfm_linattn_fwd_spin(const void* qkv, void* out, void* workspace,
     if (int rc = validate(batch, seq_len, heads, dim, in_dtype, out_dtype)) return rc;
     if (batch == 0 || seq_len == 0 || heads == 0) return KF_OK;
     const int spin = polls <= 0 || polls > kSpinLimit ? kSpinLimit : (int)polls;
+    // A cut poll limit also numbers the workgroups by ticket, as a launch
+    // beyond the device's capacity does: the members of a group then start
+    // one after another, so the early ones reach the limit while waiting.
     return linattn_run(qkv, out, workspace, workspace_bytes, batch, seq_len, heads, dim, splits, eps, in_dtype,
-                       out_dtype, false, spin, static_cast<hipStream_t>(stream));
+                       out_dtype, false, spin, static_cast<hipStream_t>(stream), spin != kSpinLimit);
 }
 
 // The split plan's arithmetic (no device call): plan[0] = split length,

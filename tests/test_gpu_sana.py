@@ -153,8 +153,9 @@ def test_workspace_contract(dim):
 def test_group_wait_give_up_writes_nan():
     """Failure handling of the fused kernel's group barrier, forced from the
     host: with the poll limit cut to two polls (the per-call test entry
-    kfm_linattn_fwd_spin), members that arrive before the rest of their group
-    stop waiting.  Each of them must set the workspace's error word and write
+    kfm_linattn_fwd_spin, which then also numbers the workgroups by ticket, so
+    a group's members start one after another), members that arrive before
+    the rest of their group stop waiting.  Each of them must set the workspace's error word and write
     NaN for its tokens; every other element must equal the normal result bit
     for bit.  The counters still return to zero, kf_linattn_check reports the
     condition (KF_E_INCOMPLETE) and clears it, and the next call is normal
@@ -229,6 +230,24 @@ def test_splits_beyond_resident_capacity(out_dtype):
     # any positive request gives a valid result, however large
     again = linear_attention(qkv.to(DEV), H, 32, output_dtype=out_dtype, splits=100000, check=True)
     torch.testing.assert_close(again.cpu().float(), ref, atol=2e-2, rtol=2e-2)
+
+
+def test_ticket_numbering_beyond_residency():
+    """A launch with more workgroups than the device holds at once (B=4,
+    H=128: 256 head pairs x 4 splits = 1024 workgroups, above the 256-512
+    slots of any output type) numbers its workgroups by ticket; it must match
+    the oracle and, to fp32 summation order, the one-split launch (256
+    workgroups, numbered by index)."""
+    B, H, N = 4, 128, 1024
+    print(f"ticket path B={B} H={H} N={N}", flush=True)
+    qkv = randn((B, N, 3, H * 32), torch.bfloat16, seed=31)
+    ref = orc.linear_attention(qkv, H, 32)
+    dev = qkv.to(DEV)
+    one = linear_attention(dev, H, 32, output_dtype=torch.float32, splits=1, check=True)
+    four = linear_attention(dev, H, 32, output_dtype=torch.float32, splits=4, check=True)
+    assert rel_fro(four, one) < 1e-5
+    check(four, ref, 1e-4)
+    check(one, ref, 1e-4)
 
 
 def test_graph_replay_and_streams():
