@@ -250,10 +250,12 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
 //            v_mfma_f32_16x16x32 with S and z held as hi+lo 16-bit pairs,
 //            rows leaving through LDS as whole-line stores.
 // Waves: (hw, th) = (head of the pair, 32-token quarter of each tile).
-// Where the time goes (MI355X, B=2, H=70, N=4096, 3 splits): phase 1 alone
-// ~19 us, phase 2 alone ~22 us, the two overlapping to ~33 us.  Phase 2 is
-// a mixed read/write stream of 128-byte spans; a probe of that traffic
-// alone reached ~4.2 TB/s at one 512-thread workgroup per CU.
+// Where the time goes (MI355X, B=2, H=70, N=4096, 3 splits, per-workgroup
+// timestamps, medians): phase 1 11.5 us, the hand-over between the phases
+// 4.6 us (combining the quarters and storing the partial 1.9, the group wait
+// 1.3, summing the partials 1.4: round trips to the coherence point that all
+// workgroups make at once), phase 2 9.6 us; the last workgroup ends 2.3 us
+// after the median one.
 // OT (fp32 output only) writes out[b][h*D + r][t] -- LiteLA.attn_matmul's
 // [B, h, d, N] result -- instead of out[b][t][h*D + r].
 //
