@@ -203,22 +203,32 @@ def test_jvp_reads_the_cached_output(dtype):
         torch.testing.assert_close(tangent.cpu(), dense, **BOUNDS[dtype])
 
 
+PEAKED = (
+    (2, 64, 80, 2, 2, 32, False, 1.0),
+    (1, 100, 150, 4, 2, 64, True, 0.6),   # GQA, bottom-right causal mask
+    (1, 40, 300, 2, 1, 128, False, 0.35),  # MQA, several key tiles
+)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
-def test_jvp_peaked_rows_recompute_the_output(dtype):
-    """With scale 1 at D = 32 most rows' rowsum(H)/l would amplify the cached
+@pytest.mark.parametrize("case", PEAKED)
+def test_jvp_peaked_rows_recompute_the_output(case, dtype):
+    """With scores this peaked most rows' rowsum(H)/l would amplify the cached
     O's rounding past the kernel's bound, so their tiles are redone with O
     recomputed from the same probabilities: tO no longer depends on `out` and
     stays within the tolerance of the fp64 oracle (the reference's formula
     with the cached O does not, on such rows)."""
-    case = (2, 64, 80, 2, 2, 32, False, 1.0)
     q, k, v, tq, tk, tv = seeded(case, dtype)
-    out, lse = flash_attention(q, k, v, return_lse=True, softmax_scale=1.0)
+    out, lse = flash_attention(q, k, v, return_lse=True, **opts(case))
     nudged = (out.float() * (1 + 2 ** -6)).to(dtype)
-    first = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, softmax_scale=1.0)
-    second = flash_attention_jvp(q, k, v, tq, tk, tv, nudged, lse, softmax_scale=1.0)
+    first = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, **opts(case))
+    second = flash_attention_jvp(q, k, v, tq, tk, tv, nudged, lse, **opts(case))
     assert torch.equal(first, second)
-    _, expected = orc.attention_jvp(*on_cpu64((q, k, v, tq, tk, tv)), softmax_scale=1.0)
+    _, expected = orc.attention_jvp(*on_cpu64((q, k, v, tq, tk, tv)), **opts(case))
     close(first, expected, dtype)
+    n_empty = empty_rows(case)
+    if n_empty:
+        assert not first[:, :n_empty].any()
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
