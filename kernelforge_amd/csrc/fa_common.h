@@ -72,7 +72,8 @@ constexpr float kRescaleThreshold = 8.0f;  // lazy rescale step of the rescaling
 // 2^-9 relative) then moves tO by at most ~2^-8 of it, about a fifth of the
 // 2e-2 tolerance (a CPU emulation of every rounding point over D = 32-128,
 // N = 64-2048 and scales 0.05-1.3 measured at most 0.24 of it).  At scale
-// 1/sqrt(D) on unit-normal inputs the product stays below ~0.6.
+// 1/sqrt(D) on unit-normal inputs the product stays below ~0.4 at 4096 keys
+// (~0.8 at 256-512 keys, where fewer keys average less).
 constexpr float kCachedOBound = 1.0f;
 
 // 256 bytes of zeros in global memory: the source of lanes whose chunk is
