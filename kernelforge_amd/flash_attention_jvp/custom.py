@@ -238,7 +238,11 @@ def flash_attention_jvp(q, k, v, tq, tk, tv, out, lse, *, softmax_scale=None, ca
     q/tq: [B, Nq, Hq, D]; k/tk/v/tv: [B, Nk, Hkv, D]; out: [B, Nq, Hq, D];
     lse: fp32 [B, Hq, Nq] in natural log, from the same primals, scale and mask.
     A ``None`` tangent denotes zero.  The result has q's dtype and out's shape.
-    Schedule arguments are validated against the reference's accepted values
+    ``out`` enters as in the reference, tO = P tv + H v - rowsum(H) out, on
+    every 128-row tile where rowsum(H) cannot amplify out's 16-bit rounding
+    past a small fraction of the tolerance; the kernel's second launch redoes
+    the other tiles (strongly peaked softmaxes) with O recomputed in fp32 from
+    the same probabilities, without reading ``out``.  Schedule arguments are validated against the reference's accepted values
     (and the gfx950 kernel's own, as ``get_jvp_config`` reports them) and
     otherwise do not change the computation: the kernel runs one tile per
     head-dim class.  The launch goes through the registered operator
