@@ -225,8 +225,13 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
 // The fused kernel (D = 32, 16-bit input).  One workgroup per (batch, head
 // pair, sequence split).  A launch whose workgroups all fit on the device at
 // once (the default split counts keep it so) numbers them by workgroup
-// index: every member a waiting workgroup needs then holds a slot or gets
-// one, whatever order the hardware starts them in.  A larger launch numbers
+// index: alone on the device, every member a waiting workgroup needs then
+// holds a slot or gets one, whatever order the hardware starts them in.
+// (Beside other launches that hold slots, index numbering relies on the
+// hardware starting a launch's workgroups in index order, as MI355X's
+// dispatcher does, to keep complete groups resident; ticket numbering does
+// not.  Out of order and oversubscribed, members could wait on each other
+// until the poll limit, and would then report it.)  A larger launch numbers
 // them by a ticket taken at start, so the members of a group start
 // consecutively: a member can only wait for members that started before it
 // or will start next, and at most one group is partly started at any time.
