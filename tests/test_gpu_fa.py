@@ -232,6 +232,26 @@ def test_jvp_peaked_rows_recompute_the_output(case, dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_jvp_recompute_only_where_marked(dtype):
+    """One launch with both kinds of 128-row tile: the first tile's queries are
+    scaled up so its softmax is peaked (its rows are redone with O
+    recomputed), the other two keep unit-normal queries (the cached O is
+    used).  Every row matches the fp64 oracle; a shifted `out` moves only the
+    rows of the cached-O tiles."""
+    b, nq, nk, h, d = 1, 384, 256, 2, 64
+    q, k, v, tq, tk, tv = seeded((b, nq, nk, h, h, d), dtype)
+    q = q.clone()
+    q[:, :128] = (q[:, :128].float() * 2).to(dtype)
+    out, lse = flash_attention(q, k, v, return_lse=True)
+    plain = flash_attention_jvp(q, k, v, tq, tk, tv, out, lse)
+    _, expected = orc.attention_jvp(*on_cpu64((q, k, v, tq, tk, tv)))
+    close(plain, expected, dtype)
+    shifted = flash_attention_jvp(q, k, v, tq, tk, tv, (out.float() + 0.125).to(dtype), lse)
+    assert torch.equal(shifted[:, :128], plain[:, :128])
+    assert not torch.equal(shifted[:, 128:], plain[:, 128:])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_uniform_score_shift_and_schedule_arguments(dtype):
     """A key tangent with q.tk the same for every key shifts all scores of a row
     by one constant: the softmax, hence O, does not move and tO = 0.  Explicit
