@@ -273,6 +273,32 @@ def test_graph_replay_and_streams():
         assert torch.equal(run(qkv), eager)
 
 
+def test_concurrent_launches_oversubscribe_the_device():
+    """Four launches of config A's shape on four streams at once (4 x 210
+    workgroups numbered by index, against 256 slots): every group's members
+    must still meet, so each result equals its eager value bit for bit and
+    no launch reports an incomplete wait."""
+    from kernelforge_amd.SANA_LinearAttention import check_status
+
+    qkvs = [randn((2, 4096, 3, 70 * 32), torch.bfloat16, seed=40 + i).to(DEV) for i in range(4)]
+    eager = [linear_attention(x, 70, 32, output_dtype=torch.bfloat16, check=True) for x in qkvs]
+    streams = [torch.cuda.Stream() for _ in qkvs]
+    outs = [None] * len(qkvs)
+    for rep in range(3):
+        print(f"concurrent launches, round {rep}", flush=True)
+        for s in streams:
+            s.wait_stream(torch.cuda.current_stream())
+        for i, (x, s) in enumerate(zip(qkvs, streams)):
+            with torch.cuda.stream(s):
+                outs[i] = linear_attention(x, 70, 32, output_dtype=torch.bfloat16)
+        for s in streams:
+            torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        check_status()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e)
+
+
 def _views(qkv, heads, dim):
     """q, k, v as LiteLA.forward makes them from a packed buffer (original.py:122-134,
     k transposed as forward passes it to attn_matmul, :140)."""
