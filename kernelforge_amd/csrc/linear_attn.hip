@@ -47,8 +47,9 @@ constexpr int kSpinLimit = 1 << 20; // polls of the group counter before giving 
 // --------------------------------------------------------------------------
 // Control words at the start of the workspace (uint32):
 //   [0]          ticket counter (start order of the fused kernel's workgroups)
-//   [1]          error word: 1 = a group barrier timed out, 2 = a ticket beyond
-//                the grid (control words not zero on entry)
+//   [1]          error word: 1 = a group barrier timed out, 2 = control words
+//                not zero on entry (a ticket beyond the grid, or a group
+//                counter above its member count)
 //   [64 + 64g]   arrivals of group g (one (batch, head pair)) at its barrier
 //   [64 + 64g+1] departures of group g from it (each group's words share no
 //                cache line with another group's, so polls do not collide)
@@ -203,7 +204,8 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
         unsigned* depart = arrive + 1;
         __hip_atomic_fetch_add(arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         int polls = 0, late = 0;
-        while (__hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < members) {
+        unsigned seen;
+        while ((seen = __hip_atomic_load(arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < members) {
             if (++polls > spin_limit) {
                 __hip_atomic_store(ctrl + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 late = 1;
@@ -211,9 +213,18 @@ __device__ __forceinline__ bool group_barrier(unsigned* ctrl, int g, unsigned me
             }
             __builtin_amdgcn_s_sleep(8);
         }
-        if (__hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1) {
+        const unsigned departed = __hip_atomic_fetch_add(depart, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (departed == members - 1) {
             __hip_atomic_store(arrive, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(depart, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // Counts no valid call produces (at most `members` arrivals and
+        // departures per call, both reset by the last to leave): the control
+        // words were not zero on entry.  Reported like a stale ticket; the
+        // partials may be incomplete, so this member writes NaN.
+        if (seen > members || departed >= members) {
+            __hip_atomic_store(ctrl + 1, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            late = 1;
         }
         *late_flag = late;
     }

@@ -150,6 +150,38 @@ def test_workspace_contract(dim):
     assert rc == 3 and b"aligned" in lib.kf_last_error()
 
 
+def test_dirty_control_words_are_reported():
+    """A workspace whose control words were never zeroed (filled with 0x7f
+    here) breaks the contract: with workgroups numbered by index, the group
+    counters then read above the member count, and the kernel reports it
+    (error word 2, KF_E_INCOMPLETE from kf_linattn_check, NaN instead of a
+    result) rather than reading incomplete partials silently.  The check
+    clears the control words, and the next call is exact again."""
+    from kernelforge_amd import _lib
+
+    lib = _lib.load()
+    B, N, H, splits = 1, 1024, 4, 4
+    qkv = randn((B, N, 3, H * 32), torch.bfloat16, seed=23).to(DEV)
+    need = int(lib.kf_linattn_workspace_bytes(B, H, 32, splits))
+    ws = torch.full((need,), 0x7F, device=DEV, dtype=torch.uint8)
+    stream = _lib.stream_of(ws)
+
+    def call():
+        out = torch.empty(B, N, H * 32, device=DEV, dtype=torch.float32)
+        _lib.check(lib.kf_linattn_fwd(_lib.ptr(qkv), _lib.ptr(out), _lib.ptr(ws), need, B, N, H, 32, splits,
+                                      1e-15, _lib.KF_BF16, _lib.KF_F32, stream), "kf_linattn_fwd")
+        torch.cuda.synchronize()
+        return out
+
+    dirty = call()
+    assert torch.isnan(dirty).any()
+    rc = lib.kf_linattn_check(_lib.ptr(ws), need, stream)
+    assert rc == 5 and b"not zero on entry" in lib.kf_last_error(), rc
+    clean = call()
+    assert lib.kf_linattn_check(_lib.ptr(ws), need, stream) == 0
+    check(clean, orc.linear_attention(qkv.cpu(), H, 32), 1e-4)
+
+
 def test_group_wait_give_up_writes_nan():
     """Failure handling of the fused kernel's group barrier, forced from the
     host: with the poll limit cut to two polls (the per-call test entry
