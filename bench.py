@@ -58,8 +58,8 @@ def _sets_for(bytes_per_set: int) -> int:
 
 
 SETTLE_MS = 100.0
-# Timed batches per workload (median reported), as SURVEY's measurement plan
-# asks; the headline RMSNorm line times exactly one batch of K steps.
+# Timed batches per workload (the median is reported, the batches are kept in
+# `repeats_us`); the headline RMSNorm line times exactly one batch of K steps.
 REPEATS = 5
 LAST_REPEATS: list = []
 

@@ -79,7 +79,7 @@ __device__ __forceinline__ void fused_tile(int blk, int tiles_m, int hg_count, i
     hg = r / gm;
 }
 
-// Round 4 accumulators (+ bias) to T.
+// Four accumulators (+ bias) rounded to T.
 template <typename T> __device__ __forceinline__ void round4(const f32x4& v, const float (&bv)[4], T (&o)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = (T)(v[i] + bv[i]);
