@@ -307,3 +307,41 @@ def test_fused_projection_path_in_a_graph():
             eager = ref(x)
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+# SANA_LinearAttention/test.py:97-153 (test_end_to_end) at the sizes of its
+# main() (test.py:182-190): batch 1, sequence lengths 1024 / 4096 / 16384,
+# channels 1152 / 2240, head dim 32, bf16 (optimized_joint_litela); fp16 runs
+# JointLiteLA, as there, here at the shortest length.
+END_TO_END = ([pytest.param(torch.bfloat16, n, c, id=f"bf16-{n}-{c}") for n in (1024, 4096, 16384) for c in (1152, 2240)]
+              + [pytest.param(torch.float16, 1024, c, id=f"fp16-1024-{c}") for c in (1152, 2240)])
+
+
+@pytest.mark.parametrize("dtype,seq_len,channels", END_TO_END)
+def test_end_to_end_reference_sizes(dtype, seq_len, channels):
+    """The eager module, the shape-specialised module, the opaque custom
+    operator traced with fullgraph=True and the HIP graph wrapper, each against
+    the CPU oracle at the reference's 2e-2 (plus the relative-norm bound)."""
+    torch._dynamo.reset()
+    torch.manual_seed(0)
+    B, heads = 1, channels // 32
+    kw = dict(heads=heads, dim=32, qk_norm=False)
+    original = LiteLA(channels, channels, **kw).to(DEV, dtype)
+    custom_cls = optimized_joint_litela if dtype == torch.bfloat16 else JointLiteLA
+    custom = custom_cls(channels, channels, batch=B, seq_len=seq_len, dtype=dtype, **kw).to(DEV, dtype)
+    custom.load_state_dict(original.state_dict())
+    custom_op = CustomOpJointLiteLA(channels, channels, batch=B, seq_len=seq_len, dtype=dtype, **kw).to(DEV, dtype)
+    custom_op.load_state_dict(original.state_dict())
+    x = torch.randn(B, seq_len, channels, generator=torch.Generator().manual_seed(9)).to(dtype).to(DEV)
+    with torch.inference_mode():
+        eager = original(x).clone()
+        actual = custom(x).clone()
+        op_out = torch.compile(custom_op, backend="aot_eager", fullgraph=True)(x).clone()
+    graph_out = CUDAGraphJointLiteLA(custom)(x).clone()
+    ref = _module_ref(original, x, False)
+    for got in (eager, actual, op_out, graph_out):
+        _close(got, ref)
+    # The operator runs the same per-shape pipeline as the eager module, and
+    # the graph replays the module it captured: both bit for bit.
+    assert torch.equal(op_out, eager)
+    assert torch.equal(graph_out, actual)
