@@ -45,6 +45,20 @@ def test_baseline_configs(B, H, N, out_name):
     print(f"B={B} H={H} N={N} out={out_name} rel_fro={err:.3g} max_abs={float((out.float().cpu()-ref).abs().max()):.3g}")
 
 
+@pytest.mark.parametrize("N", [1024, 4096, 16384])
+@pytest.mark.parametrize("C", [1152, 2240])
+def test_reference_harness_sizes(N, C):
+    """SANA_LinearAttention/test.py:50-94 at the sizes of its main()
+    (test.py:182-190): batch 1, C = 1152 / 2240 (36 / 70 heads of 32), bf16 in
+    and out, built with the reference's keyword arguments."""
+    H = C // 32
+    qkv = randn((1, N, 3, C), torch.bfloat16, seed=N + C)
+    run = qkv_attn_matmul(1, H, 32, N, dtype="bfloat16", output_dtype="bfloat16")
+    out = run(qkv.to(DEV))
+    assert out.shape == (1, N, C) and out.dtype == torch.bfloat16
+    check(out, orc.linear_attention(qkv, H, 32), 1e-2)
+
+
 @pytest.mark.parametrize("B,H,N", [(1, 1, 1), (1, 2, 63), (1, 3, 65), (2, 5, 200), (3, 4, 1000),
                                    (1, 70, 2048), (2, 36, 1024)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
