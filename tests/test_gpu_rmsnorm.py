@@ -94,6 +94,28 @@ def test_module_matches_factory():
     torch.testing.assert_close(a, b, atol=0, rtol=0)
 
 
+def test_reference_harness_defaults():
+    """rmsnorm/test.py:26-63 as its main() runs it: bf16 x [8, 512, 1024] and a
+    N(0, 1) weight, the module cast to bf16 with that weight, the two-scan fp32
+    export times the weight, and the factory kernel; the latter two within
+    2e-2 of the module, and the module against the CPU oracle."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(8, 512, 1024, generator=g).to(torch.bfloat16)
+    w = torch.randn(1024, generator=g).to(torch.bfloat16)
+    xd, wd = x.to(DEV), w.to(DEV)
+    module = RMSNorm(1024).to(DEV, torch.bfloat16)
+    module.weight.data.copy_(wd)
+    with torch.inference_mode():
+        reference = module(xd)
+    assert reference.dtype == torch.bfloat16
+    original = original_tilelang_rms_norm(xd.reshape(-1, 1024).float(), 1).reshape_as(xd) * wd
+    custom = custom_rms_norm(8, 512, 1024, module.eps, "bfloat16")(xd, wd)
+    torch.testing.assert_close(original, reference.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(custom.float(), reference.float(), rtol=2e-2, atol=2e-2)
+    assert torch.equal(custom, reference)
+    bf16_flip_check(reference.cpu().reshape(-1, 1024), orc.rmsnorm(x.reshape(-1, 1024), w, module.eps))
+
+
 def test_original_tilelang_equivalent():
     a = randn((33, 700), torch.float32, seed=5)
     b = original_tilelang_rms_norm(a.to(DEV), 1).cpu()
