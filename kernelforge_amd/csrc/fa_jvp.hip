@@ -369,6 +369,8 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
     // E = exp2(S*c + nref) and H = E * scale * tS, packed to 16 bits; their
     // rounded values are summed into l and r.
     auto probs = [&](int rb, const f32x4 (&s)[2], const f32x4 (&ts)[2], u32x2 (&ew)[2], u32x2 (&hw)[2]) {
+        // The first pair starts the sum: 0 + x is not folded under IEEE
+        // signed zeros, and E >= 0 makes the two sums equal bit for bit.
         float esum = 0.f;
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2)
@@ -376,7 +378,7 @@ __device__ __forceinline__ void fa_scan(const FaParams& p, T* kbuf0, T* kbuf1, T
             for (int j = 0; j < 2; ++j) {
                 const float e0 = fast_exp2(fmaf(s[i2][2 * j], c, nref[rb]));
                 const float e1 = fast_exp2(fmaf(s[i2][2 * j + 1], c, nref[rb]));
-                if constexpr (MODE != FA_JVP) esum += e0 + e1;
+                if constexpr (MODE != FA_JVP) esum = i2 == 0 && j == 0 ? e0 + e1 : esum + (e0 + e1);
                 const unsigned pe = Pk<T>::cvt(e0, e1);
                 ew[i2][j] = pe;
                 if constexpr (JVP) l_run[rb] = Pk<T>::sum_into(pe, l_run[rb]);
