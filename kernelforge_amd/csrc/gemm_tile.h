@@ -388,15 +388,22 @@ __device__ __forceinline__ void gemm_mainloop(const GemmSrc<T>& src, WRow wrow, 
     }
 }
 
-// Four channels of one output row: (+ bias) and one rounding to T.
-template <typename T> __device__ __forceinline__ void store4(T* dst, f32x4 v, const float (&bv)[4]) {
+// Four channels of one output row: (+ bias) and one rounding to T.  Without
+// a bias nothing is added: x + 0 is not folded under IEEE signed zeros, and
+// leaving it out keeps an all-(-0) sum at -0, as a plain product gives.
+template <bool BIAS, typename T>
+__device__ __forceinline__ void store4(T* dst, f32x4 v, const float (&bv)[4]) {
+    if constexpr (BIAS) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += bv[i];
+    }
     if constexpr (sizeof(T) == 2) {
         u32x2 out;
-        out[0] = Pk<T>::cvt(v[0] + bv[0], v[1] + bv[1]);
-        out[1] = Pk<T>::cvt(v[2] + bv[2], v[3] + bv[3]);
+        out[0] = Pk<T>::cvt(v[0], v[1]);
+        out[1] = Pk<T>::cvt(v[2], v[3]);
         *reinterpret_cast<u32x2*>(dst) = out;
     } else {
-        *reinterpret_cast<f32x4*>(dst) = f32x4{v[0] + bv[0], v[1] + bv[1], v[2] + bv[2], v[3] + bv[3]};
+        *reinterpret_cast<f32x4*>(dst) = v;
     }
 }
 

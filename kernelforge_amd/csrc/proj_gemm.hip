@@ -88,7 +88,7 @@ void proj_gemm_kernel(GemmParams p) {
 #pragma unroll
                         for (int mb = 0; mb < C::MB; ++mb) {
                             const int ml = wm * C::WM - pass * SO::ROWS + 16 * mb + (lane & 15);
-                            store4(lds + ml * SO::ROWE + nl, acc[nb][mb], bv);
+                            store4<BIAS>(lds + ml * SO::ROWE + nl, acc[nb][mb], bv);
                         }
                     }
                 }
@@ -124,7 +124,7 @@ void proj_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb) {
             const int m = m0 + wm * C::WM + 16 * mb + (lane & 15);
-            if (m < p.M) store4(y + (int64_t)m * p.ldy + n, acc[nb][mb], bv);
+            if (m < p.M) store4<BIAS>(y + (int64_t)m * p.ldy + n, acc[nb][mb], bv);
         }
     }
 }
